@@ -1,0 +1,276 @@
+#!/usr/bin/env python3
+"""Benchmark of the W8A8 DiT projection path on one MI355X.
+
+One step = the Flash-block projection chain of BASELINE config 3 at T=12288
+tokens, D=5120 (40 heads x 128), FFN 20480 with GELU-tanh, attention output
+replaced by random bf16:
+
+  rms_adaln_quant(0,1) -> QKV GEMM (N=15360) -> quantize(attn) ->
+  out-proj GEMM (N=5120) + gated residual (slot 2) -> rms_adaln_quant(3,4) ->
+  FFN-up GEMM (N=20480) + GELU-tanh -> quantize -> FFN-down GEMM (K=20480,
+  N=5120) + gated residual (slot 5)
+
+Inputs are synthetic (torch.Generator seeded with
+20261201 + config index, N(0,1) activations with 1% outlier channels x20,
+int8 weights uniform in [-127,127], per-channel scales U(1e-3,5e-3), bias
+N(0,0.02)) and resident in HBM before timing. Every kernel of every timed
+step is bracketed by HIP events on the stream it runs on (torch's current
+stream, where the library launches).
+
+Prints ONE JSON line on stdout (details on stderr):
+  value      whole-step INT8 throughput = the chain's GEMM int-ops / step time
+  roofline   the dominant kernel (FFN-up GEMM, M=12288 K=5120 N=20480) against
+             the INT8 MFMA dense peak
+  cpu_baseline  the reference's torch path (oracle/torch_path.py) on the host
+             cores, on a token slice of the same chain
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+import types
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_INT8_TOPS = 5000.0     # MI355X dense INT8 MFMA, published
+PEAK_HBM_GBS = 8000.0       # MI355X HBM3E, published
+CONFIG_INDEX = 2            # the full projection chain
+
+
+def log(*args):
+    print(*args, file=sys.stderr, flush=True)
+
+
+def parse():
+    p = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=20)
+    p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--tokens", type=int, default=12288)
+    p.add_argument("--hidden", type=int, default=5120)
+    p.add_argument("--ffn", type=int, default=20480)
+    p.add_argument("--cpu-tokens", type=int, default=256, help="token slice timed on the CPU")
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    return p.parse_args()
+
+
+def make_inputs(tokens, hidden, ffn, seed):
+    """Synthetic C3 inputs on the CPU (bf16 activations, int8 [N,K] weights)."""
+    import torch
+    g = torch.Generator().manual_seed(seed)
+
+    def activations(shape):
+        x = torch.randn(*shape, generator=g)
+        idx = torch.randperm(shape[-1], generator=g)[: max(1, round(0.01 * shape[-1]))]
+        x[..., idx] *= 20
+        return x.bfloat16()
+
+    data = types.SimpleNamespace()
+    data.x = activations((1, tokens, hidden))
+    data.attn = torch.randn(1, tokens, hidden, generator=g).bfloat16()
+    data.gamma1 = (1 + 0.05 * torch.randn(hidden, generator=g)).bfloat16()
+    data.gamma2 = (1 + 0.05 * torch.randn(hidden, generator=g)).bfloat16()
+    data.table = (0.1 * torch.randn(1, 6 * hidden, generator=g)).bfloat16()
+    data.indices = torch.zeros(tokens, dtype=torch.int64)
+    data.weights = {}
+    for name, n, k in (("qkv", 3 * hidden, hidden), ("out", hidden, hidden), ("up", ffn, hidden),
+                       ("down", hidden, ffn)):
+        w = torch.randint(-127, 128, (n, k), dtype=torch.int8, generator=g)
+        s = torch.rand(n, generator=g) * 4e-3 + 1e-3
+        b = (0.02 * torch.randn(n, generator=g)).bfloat16()
+        data.weights[name] = (w, s, b)
+    return data
+
+
+def gemm_ops(tokens, hidden, ffn):
+    return {"qkv": 2 * tokens * hidden * 3 * hidden, "out": 2 * tokens * hidden * hidden,
+            "up": 2 * tokens * hidden * ffn, "down": 2 * tokens * ffn * hidden}
+
+
+def hbm_bytes(tokens, hidden, ffn):
+    """Algorithmic HBM bytes of the row/element-wise kernels (one pass)."""
+    t, d = tokens, hidden
+    return {"norm1": 3 * t * d + 4 * t + 2 * d + 4 * d,       # x in, q out, scales, gamma, table
+            "quant_attn": 3 * t * d + 4 * t,
+            "norm2": 3 * t * d + 4 * t + 2 * d + 4 * d,
+            "quant_ffn": 3 * t * ffn + 4 * t}
+
+
+def run_gpu(args, data):
+    import torch
+    from lynnreal_omni_amd import kernels as k
+    from lynnreal_omni_amd.int8_gemm import int8_matmul
+
+    dev = torch.device("cuda:0")
+    x = data.x.to(dev)
+    attn = data.attn.reshape(-1, args.hidden).to(dev)
+    table = data.table.to(dev)
+    idx = data.indices.to(dev)
+    norm1 = types.SimpleNamespace(weight=data.gamma1.to(dev), eps=1e-6)
+    norm2 = types.SimpleNamespace(weight=data.gamma2.to(dev), eps=1e-6)
+    W = {n: (w.to(dev).t(), s.to(dev), b.to(dev)) for n, (w, s, b) in data.weights.items()}
+    torch.cuda.synchronize()
+
+    names = ["norm1", "qkv", "quant_attn", "out", "norm2", "up", "quant_ffn", "down"]
+
+    def step(ev):
+        def mark(i):
+            if ev is not None:
+                ev[i].record()
+        mark(0)
+        q1, s1 = k._rms_adaln_quant_int8(x, norm1, table, idx, 0, 1)
+        mark(1)
+        qkv = int8_matmul(q1, W["qkv"][0], s1, W["qkv"][1], W["qkv"][2])
+        mark(2)
+        qa, sa = k.quantize_rows(attn)
+        mark(3)
+        x1 = int8_matmul(qa, W["out"][0], sa, W["out"][1], W["out"][2], residual=x, table=table,
+                         indices=idx, gate_slot=2).view_as(x)
+        mark(4)
+        q2, s2 = k._rms_adaln_quant_int8(x1, norm2, table, idx, 3, 4)
+        mark(5)
+        h = int8_matmul(q2, W["up"][0], s2, W["up"][1], W["up"][2], activation="gelu_tanh")
+        mark(6)
+        q3, s3 = k.quantize_rows(h)
+        mark(7)
+        x2 = int8_matmul(q3, W["down"][0], s3, W["down"][1], W["down"][2], residual=x1, table=table,
+                         indices=idx, gate_slot=5)
+        mark(8)
+        return qkv, x2
+
+    for _ in range(args.warmup):
+        step(None)
+    torch.cuda.synchronize()
+    events = [[torch.cuda.Event(enable_timing=True) for _ in range(9)] for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for s in range(args.steps):
+        step(events[s])
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    per_kernel = {n: [] for n in names}
+    step_ms = []
+    for ev in events:
+        for i, n in enumerate(names):
+            per_kernel[n].append(ev[i].elapsed_time(ev[i + 1]))
+        step_ms.append(ev[0].elapsed_time(ev[8]))
+    return wall, step_ms, {n: statistics.mean(v) * 1e3 for n, v in per_kernel.items()}
+
+
+def run_cpu(args, data):
+    """The reference's torch path on the host cores, on a token slice."""
+    import torch
+    from oracle import torch_path as tp
+
+    cores = len(os.sched_getaffinity(0))
+    cap = int(os.environ.get("OMP_NUM_THREADS", cores) or cores)
+    threads = max(1, min(cores, cap))
+    torch.set_num_threads(threads)
+    n = min(args.cpu_tokens, args.tokens)
+    x = data.x[:, :n].contiguous()
+    attn = data.attn[:, :n].contiguous()
+    weights = {"qkv": data.weights["qkv"], "out": data.weights["out"], "up": data.weights["up"],
+               "down": data.weights["down"]}
+    weights = {kname: (w, s, b) for kname, (w, s, b) in weights.items()}
+    idx = data.indices[:n]
+
+    def once():
+        return tp.projection_chain(x, weights, data.gamma1, data.gamma2, data.table, idx, attn)
+
+    once()
+    times = []
+    budget = time.perf_counter()
+    while len(times) < 5 and (time.perf_counter() - budget < 20 or len(times) < 2):
+        t = time.perf_counter()
+        once()
+        times.append(time.perf_counter() - t)
+    med = statistics.median(times)
+    ops = sum(gemm_ops(n, args.hidden, args.ffn).values())
+    return {"value": round(ops / med / 1e12, 4), "unit": "TOPS", "cores": threads, "kind": "port",
+            "sample": f"first {n} of {args.tokens} tokens of the same chain, all four projections at "
+                      f"full width; torch CPU ops (torch._int_mm) restating model/int8.py:60-68 and "
+                      f"model/kernels.py; median of {len(times)} reps ({med * 1e3:.1f} ms/rep)",
+            "cpu": _cpu_name()}
+
+
+def _cpu_name():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only: --gpus {args.gpus} is not supported in this build "
+              "(the projection path shards by tokens with no exchange; see DESIGN.md)",
+              file=sys.stderr)
+        return 2
+    import torch
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 1
+    log(f"device {torch.cuda.get_device_name(0)}; generating C3 inputs T={args.tokens} D={args.hidden}")
+    data = make_inputs(args.tokens, args.hidden, args.ffn, 20261201 + CONFIG_INDEX)
+    wall, step_ms, kern_us = run_gpu(args, data)
+    ops = gemm_ops(args.tokens, args.hidden, args.ffn)
+    total_ops = sum(ops.values())
+    ms = statistics.mean(step_ms)
+    gemm_us = sum(kern_us[n] for n in ops)
+    up_us = kern_us["up"]
+    up_tops = ops["up"] / (up_us * 1e-6) / 1e12
+    hbm = hbm_bytes(args.tokens, args.hidden, args.ffn)
+    detail = {n: {"us": round(us, 2)} for n, us in kern_us.items()}
+    for n in ops:
+        detail[n]["tops"] = round(ops[n] / (kern_us[n] * 1e-6) / 1e12, 1)
+        detail[n]["frac_peak"] = round(detail[n]["tops"] / PEAK_INT8_TOPS, 4)
+    for n, b in hbm.items():
+        detail[n]["gbs"] = round(b / (kern_us[n] * 1e-6) / 1e9, 1)
+        detail[n]["frac_peak"] = round(detail[n]["gbs"] / PEAK_HBM_GBS, 4)
+    log(json.dumps({"kernels": detail, "wall_ms_per_step": wall * 1e3 / args.steps}, indent=1))
+    cpu = None
+    if not args.no_cpu_baseline:
+        log(f"cpu baseline on {args.cpu_tokens} tokens ...")
+        cpu = run_cpu(args, data)
+    line = {
+        "metric": "INT8 GEMM TOPS (% INT8 MFMA peak) + fused DiT-block projection us at M=12288",
+        "value": round(total_ops / (ms * 1e-3) / 1e12, 2),
+        "unit": "TOPS",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic (BASELINE.md section 4 generators, seed 20261201+2), resident in HBM",
+        "config": {"workload": "C3 Flash-block W8A8 projection chain", "tokens": args.tokens,
+                   "hidden": args.hidden, "heads": "40x128", "ffn": args.ffn,
+                   "ffn_activation": "gelu_tanh", "gemm_ops_per_step": total_ops,
+                   "parallelism": "single GPU"},
+        "block_us": round(ms * 1e3, 1),
+        "pct_int8_peak": round(100 * total_ops / (ms * 1e-3) / 1e12 / PEAK_INT8_TOPS, 2),
+        "gemm_tops": round(total_ops / (gemm_us * 1e-6) / 1e12, 1),
+        "kernels": detail,
+        "roofline": {"kernel": "int8 GEMM FFN-up M=12288 K=5120 N=20480 (+GELU epilogue)",
+                     "bound": "mfma", "achieved": round(up_tops, 1), "peak": PEAK_INT8_TOPS,
+                     "unit": "TFLOP/s", "frac": round(up_tops / PEAK_INT8_TOPS, 4),
+                     "traffic": None, "us": round(up_us, 2)},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,173 @@
+/*
+ * lynnreal_amd.h - C ABI of the MI355X (gfx950) W8A8 DiT projection path.
+ *
+ * The reference (LynnReal-Omni) exposes this path as Python functions that
+ * launch Triton kernels; it has no FFI. Each entry point below replaces one
+ * of those functions and cites it (paths relative to the reference checkout).
+ * The Python host layer in lynnreal_omni_amd/ keeps the reference's Python
+ * signatures and calls these entry points through ctypes.
+ *
+ * Conventions shared by every entry point:
+ *   - All tensor arguments are raw device pointers. bf16 tensors are passed as
+ *     `const void*` / `void*` and hold IEEE bfloat16 bit patterns.
+ *   - Tensors are dense and row-major unless a stride argument says otherwise.
+ *   - The library never allocates or frees device memory: the caller owns
+ *     every input and output buffer (the reference allocates outputs with
+ *     torch.empty on the input's device, kernels.py:21-22, int8_gemm.py:134).
+ *   - `stream` is a hipStream_t (NULL = the default stream). Work is enqueued
+ *     on it with no host synchronisation.
+ *   - Every entry point returns an LR_* status. On failure lr_last_error()
+ *     returns a message for the calling thread.
+ *   - `indices` index rows of an adaLN table. Values outside [0, table_rows)
+ *     are clamped into that range so that a bad index can never read outside
+ *     the table (the reference performs no check).
+ */
+#ifndef LYNNREAL_AMD_H
+#define LYNNREAL_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define LR_ABI_VERSION 1
+
+/* Status codes. The Python layer maps them to exceptions:
+ * EINVAL -> ValueError, EUNSUPPORTED -> RuntimeError("... not supported"),
+ * ENOMEM -> torch.cuda.OutOfMemoryError, EHIP -> RuntimeError. */
+#define LR_OK 0
+#define LR_EINVAL 1
+#define LR_EUNSUPPORTED 2
+#define LR_EHIP 3
+#define LR_ENOMEM 4
+
+/* GEMM epilogues (lr_int8_gemm `epilogue`). */
+#define LR_EPI_BF16 0           /* bf16(((float)acc*row_scale)*col_scale + bias)      */
+#define LR_EPI_GELU_TANH 1      /* bf16(gelu_tanh(y)), y = the LR_EPI_BF16 value       */
+#define LR_EPI_GATED_RESIDUAL 2 /* bf16(x + bf16(gate*y)), y = the LR_EPI_BF16 value   */
+#define LR_EPI_RAW_INT32 3      /* int32 accumulators, no scaling                      */
+
+/* GEMM tile configurations (lr_int8_gemm `tile`). */
+#define LR_TILE_AUTO 0
+#define LR_TILE_256x256 1
+#define LR_TILE_256x128 2
+#define LR_TILE_128x256 3
+#define LR_TILE_128x128 4
+#define LR_TILE_64x128 5
+#define LR_TILE_GENERIC 6 /* any strides / K; slow, used when the fast path cannot run */
+
+/* Library version; bumped whenever a signature below changes. */
+int lr_abi_version(void);
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* lr_last_error(void);
+
+/* 1 if `device` is a gfx950 GPU this library was built for, else 0.
+ * Replaces the capability gate of model/acceleration.py:5-18. */
+int lr_device_supported(int device);
+
+/* Per-row symmetric INT8 quantizer.
+ * Replaces model/kernels.py:19-24 (quantize_rows) with the arithmetic of the
+ * torch path model/int8.py:66-67:
+ *   s[r] = max(max_c |x[r,c]|, 1e-8f) / 127.0f
+ *   q[r,c] = clamp(rint_half_even(x[r,c] / s[r]), -127, 127)
+ * x bf16 [rows, width]; q int8 [rows, width]; scales fp32 [rows]. */
+int lr_quantize_rows(const void* x, int64_t rows, int64_t width, int8_t* q, float* scales,
+                     void* stream);
+
+/* INT8 x INT8 -> INT32 GEMM with a fused epilogue.
+ * Replaces model/int8_gemm.py:96-163 (int8_matmul) and its Triton kernel
+ * model/int8_gemm.py:13-46:
+ *   acc[m,n] = sum_k A[m,k] * B[k,n]                  (exact int32)
+ *   y[m,n]   = bf16(((float)acc * row_scale[m]) * col_scale[n] + bias[n])
+ * A int8 [M,K] row-major. B int8 with B[k,n] at b[k*b_stride_k + n*b_stride_n];
+ * the weight layout of Int8Linear (a [K,N] view of [N,K] storage) has
+ * b_stride_k = 1, b_stride_n = K and takes the MFMA fast path.
+ * row_scale fp32 [M]; col_scale fp32 [N]; bias bf16 [N] or NULL.
+ * c: bf16 [M,N] (or int32 [M,N] for LR_EPI_RAW_INT32).
+ * Gated residual (LR_EPI_GATED_RESIDUAL; model/kernels.py:131-153 applied to
+ * the GEMM output): residual bf16 [M,N], table bf16 [table_rows, table_width],
+ * indices int64 [sequence]; row m uses table row indices[m % sequence] and
+ * gate = table[row, gate_slot*N + n]. Unused arguments may be NULL/0.
+ * tile: LR_TILE_* (LR_TILE_AUTO picks by shape). */
+int lr_int8_gemm(const int8_t* a, const int8_t* b, int64_t b_stride_k, int64_t b_stride_n,
+                 int64_t m, int64_t n, int64_t k, const float* row_scale, const float* col_scale,
+                 const void* bias, void* c, int epilogue, const void* residual, const void* table,
+                 int64_t table_rows, int64_t table_width, const int64_t* indices,
+                 int64_t sequence, int gate_slot, int tile, void* stream);
+
+/* Stand-alone INT32 -> bf16 dequant epilogue.
+ * Replaces model/kernels.py:41-46 (int8_epilogue):
+ *   out[m,n] = bf16(((float)acc[m,n] * a_scale[m]) * w_scale[n] + bias[n]).
+ * acc int32 [M,N]; a_scale fp32 [M]; w_scale fp32 [N]; bias bf16 [N] or NULL. */
+int lr_int8_epilogue(const int32_t* acc, const float* a_scale, const float* w_scale,
+                     const void* bias, void* out, int64_t m, int64_t n, void* stream);
+
+/* Fused RMSNorm + adaLN modulate, bf16 out.
+ * Replaces model/kernels.py:260-272 (_rms_adaln) / kernel :48-78. Row r uses
+ * token r % sequence and table row tr = indices[token]:
+ *   ss = sum_c x^2 (fp32, fixed order: see lr_rms_adaln_quant)
+ *   rr = 1 / sqrt(ss / hidden + eps)
+ *   n  = bf16((x * rr) * weight[c])
+ *   y  = bf16(bf16(n * bf16(1 + table[tr, scale_slot*hidden + c]))
+ *             + table[tr, shift_slot*hidden + c])
+ * x bf16 [rows, hidden]; weight bf16 [hidden]; out bf16 [rows, hidden]. */
+int lr_rms_adaln(const void* x, const void* weight, const void* table, const int64_t* indices,
+                 void* out, int64_t rows, int64_t sequence, int64_t hidden, int64_t table_rows,
+                 int64_t table_width, int shift_slot, int scale_slot, float eps, void* stream);
+
+/* Fused RMSNorm + adaLN modulate + per-row INT8 quantization.
+ * Replaces model/kernels.py:275-289 (_rms_adaln_quant_int8) / kernel :81-128.
+ * y as in lr_rms_adaln, then q/scales as in lr_quantize_rows.
+ * The sum of squares has one defined order so that results are reproducible:
+ * the row is cut into 8-element chunks; chunk j is accumulated into slot
+ * j % 256 (chunks in increasing j, elements in order, fp32); the 256 slots are
+ * then combined by s[i] += s[i + h] for h = 128, 64, ..., 1. */
+int lr_rms_adaln_quant(const void* x, const void* weight, const void* table,
+                       const int64_t* indices, int8_t* q, float* scales, int64_t rows,
+                       int64_t sequence, int64_t hidden, int64_t table_rows, int64_t table_width,
+                       int shift_slot, int scale_slot, float eps, void* stream);
+
+/* Gated residual + RMSNorm + adaLN modulate + INT8 quantization.
+ * Replaces model/kernels.py:405-419 (residual_rms_quant; branch :101-105):
+ *   x' = bf16(x + bf16(table[tr, 2*hidden + c] * u)), stored to residual_out,
+ * then lr_rms_adaln_quant on x' with shift slot 3 and scale slot 4. */
+int lr_residual_rms_quant(const void* x, const void* update, const void* weight,
+                          const void* table, const int64_t* indices, void* residual_out,
+                          int8_t* q, float* scales, int64_t rows, int64_t sequence,
+                          int64_t hidden, int64_t table_rows, int64_t table_width, float eps,
+                          void* stream);
+
+/* Gated residual. Replaces model/kernels.py:292-304 (_gated_residual) /
+ * kernel :131-153:  out = bf16(x + bf16(table[tr, gate_slot*hidden + c] * u)).
+ * x, u, out bf16 [rows, hidden]. */
+int lr_gated_residual(const void* x, const void* update, const void* table,
+                      const int64_t* indices, void* out, int64_t rows, int64_t sequence,
+                      int64_t hidden, int64_t table_rows, int64_t table_width, int gate_slot,
+                      void* stream);
+
+/* SwiGLU. Replaces model/kernels.py:307-315 (_swiglu) / kernel :156-166:
+ *   out[r,c] = bf16(v * bf16(g * sigmoid(g))), v = p[r,c], g = p[r,inner+c].
+ * p bf16 [rows, 2*inner]; out bf16 [rows, inner]. */
+int lr_swiglu(const void* p, void* out, int64_t rows, int64_t inner, void* stream);
+
+/* SwiGLU + INT8 quantization. Replaces model/kernels.py:318-328
+ * (_swiglu_quant_int8) / kernel :169-185:
+ *   a = bf16(v * bf16(g * sigmoid(g))), then q/scales as lr_quantize_rows.
+ * q int8 [rows, inner]; scales fp32 [rows]. */
+int lr_swiglu_quant(const void* p, int8_t* q, float* scales, int64_t rows, int64_t inner,
+                    void* stream);
+
+/* Element-wise GELU (tanh approximation), bf16 in and out:
+ *   out = bf16(0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3)))).
+ * The reference has no in-tree kernel for it; its only GELU-tanh INT8 path is
+ * comfy-kitchen's int8_linear(input_act="gelu_tanh"), exercised at
+ * comfyui/custom_nodes/ComfyUI-LynnReal/tools/verify_sampling_safety.py:59. */
+int lr_gelu_tanh(const void* x, void* out, int64_t count, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LYNNREAL_AMD_H */

@@ -1,0 +1,129 @@
+"""ctypes binding of liblynnreal_amd.so, the gfx950 C ABI (include/lynnreal_amd.h).
+
+The library is loaded lazily on first use. There is no fallback: if the
+library is missing or the device is not a gfx950 GPU, every call raises.
+
+Status codes map to the exception types the reference's error policy expects
+(model/acceleration.py:49-56 treats "not supported" messages as recoverable
+and never recovers from out-of-memory):
+  LR_EINVAL       -> ValueError
+  LR_EUNSUPPORTED -> RuntimeError("... not supported")
+  LR_ENOMEM       -> torch.cuda.OutOfMemoryError
+  LR_EHIP         -> RuntimeError
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import pathlib
+import threading
+
+import torch
+
+LIBRARY = pathlib.Path(__file__).resolve().parent / "liblynnreal_amd.so"
+
+LR_OK, LR_EINVAL, LR_EUNSUPPORTED, LR_EHIP, LR_ENOMEM = 0, 1, 2, 3, 4
+EPI_BF16, EPI_GELU_TANH, EPI_GATED_RESIDUAL, EPI_RAW_INT32 = 0, 1, 2, 3
+TILE_AUTO, TILE_256x256, TILE_256x128, TILE_128x256, TILE_128x128, TILE_64x128, TILE_GENERIC = range(7)
+ABI_VERSION = 1
+
+_P = ctypes.c_void_p
+_I64 = ctypes.c_int64
+_I32 = ctypes.c_int
+_F32 = ctypes.c_float
+
+# name -> argument types (every entry point returns int).
+SIGNATURES = {
+    "lr_quantize_rows": [_P, _I64, _I64, _P, _P, _P],
+    "lr_int8_gemm": [_P, _P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _I32, _P, _P, _I64,
+                     _I64, _P, _I64, _I32, _I32, _P],
+    "lr_int8_epilogue": [_P, _P, _P, _P, _P, _I64, _I64, _P],
+    "lr_rms_adaln": [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I32, _I32, _F32, _P],
+    "lr_rms_adaln_quant": [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I32, _I32,
+                           _F32, _P],
+    "lr_residual_rms_quant": [_P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64,
+                              _F32, _P],
+    "lr_gated_residual": [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I32, _P],
+    "lr_swiglu": [_P, _P, _I64, _I64, _P],
+    "lr_swiglu_quant": [_P, _P, _P, _I64, _I64, _P],
+    "lr_gelu_tanh": [_P, _P, _I64, _P],
+    "lr_device_supported": [_I32],
+    "lr_abi_version": [],
+    "lr_gemm_set_group_m": [_I32],
+}
+
+_lock = threading.Lock()
+_lib = None
+
+
+def library_path() -> pathlib.Path:
+    return pathlib.Path(os.environ.get("LYNNREAL_AMD_LIBRARY", LIBRARY))
+
+
+def load() -> ctypes.CDLL:
+    """Load the HIP library (once) and declare its prototypes."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        path = library_path()
+        if not path.exists():
+            raise RuntimeError(
+                f"{path} is missing: build it with `python -m lynnreal_omni_amd.build` "
+                "(the W8A8 path has no CPU fallback)")
+        lib = ctypes.CDLL(str(path))
+        for name, argtypes in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.argtypes = argtypes
+            fn.restype = ctypes.c_int
+        lib.lr_last_error.argtypes = []
+        lib.lr_last_error.restype = ctypes.c_char_p
+        if lib.lr_abi_version() != ABI_VERSION:
+            raise RuntimeError(f"{path} has ABI {lib.lr_abi_version()}, expected {ABI_VERSION}")
+        _lib = lib
+    return _lib
+
+
+def raise_for(status: int, name: str) -> None:
+    if status == LR_OK:
+        return
+    message = f"{name}: {load().lr_last_error().decode(errors='replace')}"
+    if status == LR_EINVAL:
+        raise ValueError(message)
+    if status == LR_EUNSUPPORTED:
+        raise RuntimeError(message if "not supported" in message else message + " (not supported)")
+    if status == LR_ENOMEM:
+        raise torch.cuda.OutOfMemoryError(message)
+    raise RuntimeError(message)
+
+
+def call(name: str, *args) -> None:
+    """Call entry point `name` and raise on a non-zero status."""
+    raise_for(getattr(load(), name)(*args), name)
+
+
+_checked_devices: dict[int, bool] = {}
+
+
+def check_device(t: torch.Tensor) -> None:
+    """Raise unless `t` lives on a gfx950 GPU the library supports."""
+    if t.device.type != "cuda":
+        raise ValueError(f"the W8A8 HIP path needs GPU tensors, got a tensor on {t.device}")
+    index = t.device.index if t.device.index is not None else torch.cuda.current_device()
+    ok = _checked_devices.get(index)
+    if ok is None:
+        ok = _checked_devices[index] = bool(load().lr_device_supported(index))
+    if not ok:
+        raise RuntimeError(f"device {index} ({torch.cuda.get_device_name(index)}) is not supported: "
+                           "liblynnreal_amd.so is built for gfx950 only")
+
+
+def stream(t: torch.Tensor) -> int:
+    """The caller's current HIP stream on t's device (Triton's launch behaviour)."""
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()

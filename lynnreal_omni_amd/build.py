@@ -1,0 +1,76 @@
+"""Build liblynnreal_amd.so, the gfx950 HIP library of the W8A8 path, in-tree.
+
+Usage: python -m lynnreal_omni_amd.build  (or build() from Python).
+
+Every .hip file under csrc/ is compiled for gfx950 only, in parallel, and
+linked into lynnreal_omni_amd/liblynnreal_amd.so. The library is written to
+a temporary name and renamed into place, so a process that has the old one
+loaded keeps a valid mapping.
+"""
+from __future__ import annotations
+
+import concurrent.futures
+import os
+import pathlib
+import shutil
+import subprocess
+
+HERE = pathlib.Path(__file__).resolve().parent
+ROOT = HERE.parent
+CSRC = HERE / "csrc"
+OBJ = HERE / "_build"
+LIBRARY = HERE / "liblynnreal_amd.so"
+
+ARCH = "gfx950"
+FLAGS = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    # IEEE semantics: no FMA contraction, correctly rounded fp32 divide/sqrt.
+    "-ffp-contract=off",
+    "-fhip-fp32-correctly-rounded-divide-sqrt",
+    # Never emit packed fp32 arithmetic (device pass; the host pass ignores it).
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wall",
+    f"-I{ROOT / 'include'}",
+    f"-I{CSRC}",
+]
+
+
+def hipcc() -> str:
+    path = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
+    if not os.path.exists(path):
+        raise RuntimeError("hipcc not found; the HIP toolchain is required to build")
+    return path
+
+
+def _compile(src: pathlib.Path, extra: list[str]) -> pathlib.Path:
+    obj = OBJ / (src.stem + ".o")
+    cmd = [hipcc(), *FLAGS, *extra, "-c", str(src), "-o", str(obj)]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"hipcc failed on {src.name}:\n{proc.stderr}")
+    return obj
+
+
+def build(extra: list[str] | None = None, jobs: int = 8) -> pathlib.Path:
+    """Compile every csrc/*.hip for gfx950 and link the shared library."""
+    extra = list(extra or [])
+    OBJ.mkdir(exist_ok=True)
+    sources = sorted(CSRC.glob("*.hip"))
+    if not sources:
+        raise RuntimeError(f"no HIP sources under {CSRC}")
+    with concurrent.futures.ThreadPoolExecutor(max_workers=jobs) as pool:
+        objects = list(pool.map(lambda s: _compile(s, extra), sources))
+    tmp = LIBRARY.with_name(LIBRARY.name + f".tmp{os.getpid()}")
+    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objects)]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"link failed:\n{proc.stderr}")
+    os.replace(tmp, LIBRARY)
+    return LIBRARY
+
+
+if __name__ == "__main__":
+    print(build())

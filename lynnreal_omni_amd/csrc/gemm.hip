@@ -1,0 +1,508 @@
+// gemm.hip - INT8 x INT8 -> INT32 GEMM on CDNA4 MFMA with fused epilogues.
+//
+// Restates model/int8_gemm.py:13-46 (_gemm) and :84-92 (_torch_matmul):
+//   acc[m,n] = sum_k A[m,k] * W[n,k]                        (exact int32)
+//   y[m,n]   = bf16(((float)acc * row_scale[m]) * col_scale[n] + bias[n])
+// plus GELU-tanh and gated-residual epilogues and a raw-int32 debug output.
+//
+// Fast kernel (A [M,K] row-major, W [N,K] row-major, K % 16 == 0):
+//  * Block tile BM x BN, K step 64, 256 threads = 4 waves in a WAVES_M x
+//    WAVES_N grid; each wave owns a (BM/WAVES_M) x (BN/WAVES_N) sub-tile made
+//    of 16x16 MFMA tiles (v_mfma_i32_16x16x64_i8), accumulators in AGPRs.
+//  * LDS holds STAGES k-steps. Each k-step of A (and of W) is stored as 1 KB
+//    "fragments" of 16 rows x 64 k, laid out in exactly the order the MFMA
+//    wants its operand: lane l's 16 bytes (row l%16, k 16*(l/16)..+15) sit at
+//    byte 16*l. A fragment is therefore read with one conflict-free
+//    ds_read_b128 per lane and written with one 16-byte-per-lane
+//    buffer_load ... lds (global -> LDS without touching VGPRs).
+//  * Buffer descriptors bound each block's rows, so rows past M/N and k past
+//    K read as zero: no masking in the main loop, tails are exact.
+//  * The MFMA is issued as W_frag x A_frag, so lane l ends with row l%16 and
+//    4 consecutive columns of C: the epilogue writes 8-byte bf16 groups.
+//  * Workgroups are dispatched round-robin over the 8 XCDs; the tile order
+//    is renumbered so that each XCD walks a contiguous, M-grouped range of
+//    tiles and its 4 MB L2 holds the A and W panels its CUs share.
+// Generic kernel: any W strides / K, LDS-tiled int32 dot products (slow path
+// used only when the fast kernel cannot run).
+#include "lr_device.h"
+#include "lr_runtime.h"
+
+namespace lr {
+namespace {
+
+struct GemmArgs {
+  const int8_t* a;
+  const int8_t* b;
+  const float* rs;
+  const float* cs;
+  const uint16_t* bias;
+  void* c;
+  const uint16_t* resid;
+  const uint16_t* table;
+  const int64_t* indices;
+  int64_t m, n, k;
+  int64_t b_sk, b_sn;
+  int64_t table_rows, table_width, sequence;
+  int gate_slot;
+  int tiles_m, tiles_n, group_m;
+  int nvec;  // N % 4 == 0 and C/bias/col_scale/residual aligned for 4-wide access
+};
+
+enum { EPI_BF16 = LR_EPI_BF16, EPI_GELU = LR_EPI_GELU_TANH, EPI_GATED = LR_EPI_GATED_RESIDUAL,
+       EPI_RAW = LR_EPI_RAW_INT32 };
+
+// ------------------------------------------------------------ epilogue ----
+// The bf16 GEMM value, model/int8_gemm.py:42-45 / :89-92 (no FMA contraction).
+template <bool BIAS>
+__device__ __forceinline__ float dequant(int acc, float rs, float cs, float bias) {
+  float v = ((float)acc * rs) * cs;
+  if (BIAS) v = v + bias;
+  return v;
+}
+
+// Final value of one output element for the bf16-producing epilogues.
+// gate/x are only read for EPI_GATED.
+template <int EPI>
+__device__ __forceinline__ float finish(float v, float gate, float x) {
+  if (EPI == EPI_GELU) return fast_gelu_tanh(round_bf(v));
+  if (EPI == EPI_GATED) return x + round_bf(gate * round_bf(v));
+  return v;
+}
+
+__device__ __forceinline__ int64_t table_row(const GemmArgs& p, int64_t row) {
+  return clamp_index(p.indices[row % p.sequence], p.table_rows);
+}
+
+// Stores one element (any shape / alignment).
+template <int EPI, bool BIAS>
+__device__ __forceinline__ void store_scalar(const GemmArgs& p, int64_t row, int64_t col,
+                                             int acc) {
+  const int64_t o = row * p.n + col;
+  if (EPI == EPI_RAW) {
+    static_cast<int32_t*>(p.c)[o] = acc;
+    return;
+  }
+  const float bias = BIAS ? bf_to_f(p.bias[col]) : 0.0f;
+  float v = dequant<BIAS>(acc, p.rs[row], p.cs[col], bias);
+  float gate = 0.0f, x = 0.0f;
+  if (EPI == EPI_GATED) {
+    gate = bf_to_f(p.table[table_row(p, row) * p.table_width + (int64_t)p.gate_slot * p.n + col]);
+    x = bf_to_f(p.resid[o]);
+  }
+  v = finish<EPI>(v, gate, x);
+  static_cast<uint16_t*>(p.c)[o] = (uint16_t)(pack_bf2(v, 0.0f) & 0xffffu);
+}
+
+// ----------------------------------------------------------- tile order ----
+__device__ __forceinline__ void tile_coords(const GemmArgs& p, int& tm, int& tn) {
+  const int pid = blockIdx.x;
+  const int total = p.tiles_m * p.tiles_n;
+  const int xcd = pid & 7, local = pid >> 3;
+  const int q = total >> 3, r = total & 7;
+  const int lid = (xcd < r ? xcd * (q + 1) : r * (q + 1) + (xcd - r) * q) + local;
+  const int span = p.group_m * p.tiles_n;
+  const int g = lid / span;
+  const int first = g * p.group_m;
+  const int gm = min(p.tiles_m - first, p.group_m);
+  const int within = lid - g * span;
+  tm = first + within % gm;
+  tn = within / gm;
+}
+
+typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+// 16 bytes per lane from a buffer resource straight into LDS: lane l writes
+// lds + 16*l. Offsets past the resource's num_records read as zero.
+// (Device-only wrapper: lambdas in kernels are host+device, and the host pass
+// must not see the builtin.)
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t rsrc, void* lds, uint32_t voffset) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_ptr_t)lds, 16, voffset, 0, 0, 0);
+}
+
+__device__ __forceinline__ void wait_vmcnt(int n) {
+  // s_waitcnt with expcnt/lgkmcnt at their maximum: wait on vmcnt only.
+  // vmcnt is 6 bits on gfx9: [3:0] and [15:14].
+  switch (n) {
+#define LR_VM(N) \
+  case N: __builtin_amdgcn_s_waitcnt(((N) & 15) | (((N) >> 4) << 14) | 0x70 | 0xf00); break;
+    LR_VM(0) LR_VM(1) LR_VM(2) LR_VM(3) LR_VM(4) LR_VM(5) LR_VM(6) LR_VM(7) LR_VM(8)
+    LR_VM(9) LR_VM(10) LR_VM(11) LR_VM(12) LR_VM(13) LR_VM(14) LR_VM(15) LR_VM(16)
+    LR_VM(17) LR_VM(18) LR_VM(19) LR_VM(20) LR_VM(21) LR_VM(22) LR_VM(23) LR_VM(24)
+    LR_VM(25) LR_VM(26) LR_VM(27) LR_VM(28) LR_VM(29) LR_VM(30) LR_VM(31) LR_VM(32)
+#undef LR_VM
+    default: __builtin_amdgcn_s_waitcnt(0x70 | 0xf00); break;
+  }
+}
+
+// ----------------------------------------------------------- fast GEMM ----
+template <int BM, int BN, int WAVES_M, int STAGES, int EPI, bool BIAS>
+__global__ __launch_bounds__(256) void gemm_fast(GemmArgs p) {
+  constexpr int BK = 64;
+  constexpr int WAVES_N = 4 / WAVES_M;
+  constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N;
+  constexpr int FM = WM / 16, FN = WN / 16;
+  constexpr int A_BYTES = BM * BK, B_BYTES = BN * BK;
+  constexpr int STAGE_BYTES = A_BYTES + B_BYTES;
+  constexpr int A_LOADS = BM / 64, B_LOADS = BN / 64;  // 1 KB fragments per wave per k-step
+  constexpr int LOADS = A_LOADS + B_LOADS;
+  static_assert(WAVES_M * WAVES_N == 4, "4 waves");
+  static_assert(BM % 64 == 0 && BN % 64 == 0 && FM % 4 == 0 && FN >= 1, "tile shape");
+  static_assert(STAGES >= 3 && LOADS * (STAGES - 2) <= 32, "stages / vmcnt budget");
+  __shared__ __attribute__((aligned(1024))) char smem[STAGES * STAGE_BYTES];
+
+  int tm, tn;
+  tile_coords(p, tm, tn);
+  const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int wm = wave / WAVES_N, wn = wave % WAVES_N;
+  const int64_t K = p.k;
+  const int KT = (int)((K + BK - 1) / BK);
+
+  const int64_t rows_a = min((int64_t)BM, p.m - m0);
+  const int64_t rows_b = min((int64_t)BN, p.n - n0);
+  const __amdgpu_buffer_rsrc_t ra =
+      __builtin_amdgcn_make_buffer_rsrc((void*)(p.a + m0 * K), (short)0, (int)(rows_a * K), 0x00020000);
+  const __amdgpu_buffer_rsrc_t rb =
+      __builtin_amdgcn_make_buffer_rsrc((void*)(p.b + n0 * K), (short)0, (int)(rows_b * K), 0x00020000);
+
+  const int kchunk = (lane >> 4) * 16;
+  uint32_t a_off[A_LOADS], b_off[B_LOADS];
+#pragma unroll
+  for (int i = 0; i < A_LOADS; ++i)
+    a_off[i] = (uint32_t)(((wave * A_LOADS + i) * 16 + (lane & 15)) * K + kchunk);
+#pragma unroll
+  for (int j = 0; j < B_LOADS; ++j)
+    b_off[j] = (uint32_t)(((wave * B_LOADS + j) * 16 + (lane & 15)) * K + kchunk);
+
+  auto issue = [&](int kt, int stage) {
+    const bool kin = (int64_t)kt * BK + kchunk < K;
+    const uint32_t kofs = (uint32_t)kt * BK;
+    char* sa = smem + stage * STAGE_BYTES;
+    char* sb = sa + A_BYTES;
+#pragma unroll
+    for (int i = 0; i < A_LOADS; ++i)
+      dma16(ra, sa + (wave * A_LOADS + i) * 1024, kin ? a_off[i] + kofs : 0x80000000u);
+#pragma unroll
+    for (int j = 0; j < B_LOADS; ++j)
+      dma16(rb, sb + (wave * B_LOADS + j) * 1024, kin ? b_off[j] + kofs : 0x80000000u);
+  };
+
+  auto read_a = [&](int kt, int i) -> v4i {
+    const char* sa = smem + (kt % STAGES) * STAGE_BYTES;
+    return *reinterpret_cast<const v4i*>(sa + (wm * FM + i) * 1024 + lane * 16);
+  };
+  auto read_w = [&](int kt, int j) -> v4i {
+    const char* sb = smem + (kt % STAGES) * STAGE_BYTES + A_BYTES;
+    return *reinterpret_cast<const v4i*>(sb + (wn * FN + j) * 1024 + lane * 16);
+  };
+
+  v4i acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j) acc[i][j] = v4i{0, 0, 0, 0};
+
+  // All waves wait for their own DMA of a k-step, then meet at the barrier:
+  // after it the k-step is complete in LDS, and every wave has finished the
+  // previous iteration (so the buffer it read may be overwritten).
+  auto sync_stage = [&](int pending_after) {
+    wait_vmcnt(pending_after * LOADS);
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  // Register schedule: W fragments are double-buffered per k-step (wf[parity]);
+  // A fragments rotate through 4 registers, read two MFMA rows ahead. During
+  // k-step kt the reads for k-step kt+1 (its first two A rows and all W
+  // fragments) are already issued, so the MFMA pipe never waits on LDS.
+  v4i wf[2][FN], af[4];
+
+  // Prologue: DMA k-steps 0 .. STAGES-2, then k-step 0's first fragments.
+#pragma unroll
+  for (int s = 0; s < STAGES - 1; ++s)
+    if (s < KT) issue(s, s);
+  if (KT > 0) {
+    sync_stage(min(STAGES - 2, KT - 1));
+#pragma unroll
+    for (int j = 0; j < FN; ++j) wf[0][j] = read_w(0, j);
+    af[0] = read_a(0, 0);
+    af[1] = read_a(0, 1);
+  }
+
+  // One k-step. next: a k-step kt+1 exists (sync it, prefetch its
+  // fragments); dma: k-step kt+STAGES-1 exists (start its DMA). Every call
+  // passes constants, so after inlining each phase below is branch-free.
+  auto step = [&](bool next, bool dma, int kt, int pending) __attribute__((always_inline)) {
+    if (next) sync_stage(pending);
+    if (dma) issue(kt + STAGES - 1, (kt + STAGES - 1) % STAGES);
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+      const int r = i + 2;
+      if (r < FM) af[r % 4] = read_a(kt, r);
+      else if (next) af[r % 4] = read_a(kt + 1, r - FM);
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+        if (next && j * FM / FN == i) wf[1][j] = read_w(kt + 1, j);
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wf[0][j], af[i % 4], acc[i][j], 0, 0, 0);
+    }
+    if (next) {
+#pragma unroll
+      for (int j = 0; j < FN; ++j) wf[0][j] = wf[1][j];
+    }
+  };
+  int kt = 0;
+  for (; kt + STAGES - 1 < KT; ++kt) step(true, true, kt, STAGES - 3);  // steady state
+  for (; kt + 1 < KT; ++kt) step(true, false, kt, KT - 2 - kt);         // DMA drained
+  if (kt < KT) step(false, false, kt, 0);                               // last k-step
+
+  // Epilogue. Lane l holds, for MFMA tile (i, j), row wm*WM + 16i + l%16 and
+  // columns wn*WN + 16j + 4*(l/16) + 0..3.
+  const int lr_ = lane & 15, lg = lane >> 4;
+  int64_t rows[FM];
+  float rsv[FM];
+  int64_t trow[FM];
+#pragma unroll
+  for (int i = 0; i < FM; ++i) {
+    rows[i] = m0 + wm * WM + 16 * i + lr_;
+    const bool ok = rows[i] < p.m;
+    rsv[i] = (EPI != EPI_RAW && ok) ? p.rs[rows[i]] : 0.0f;
+    trow[i] = (EPI == EPI_GATED && ok) ? table_row(p, rows[i]) : 0;
+  }
+#pragma unroll
+  for (int j = 0; j < FN; ++j) {
+    // Keep the column groups apart: hoisting every accumulator read to the
+    // top would need all 256 accumulators in VGPRs at once.
+    __builtin_amdgcn_sched_barrier(0);
+    const int64_t col = n0 + wn * WN + 16 * j + 4 * lg;
+    if (p.nvec) {
+      if (col >= p.n) continue;
+      if (EPI == EPI_RAW) {
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+          if (rows[i] < p.m)
+            *reinterpret_cast<v4i*>(static_cast<int32_t*>(p.c) + rows[i] * p.n + col) = acc[i][j];
+        continue;
+      }
+      const float4 cs = *reinterpret_cast<const float4*>(p.cs + col);
+      float b0 = 0.f, b1 = 0.f, b2 = 0.f, b3 = 0.f;
+      if (BIAS) {
+        const uint2 bb = *reinterpret_cast<const uint2*>(p.bias + col);
+        b0 = bf_lo(bb.x); b1 = bf_hi(bb.x); b2 = bf_lo(bb.y); b3 = bf_hi(bb.y);
+      }
+#pragma unroll
+      for (int i = 0; i < FM; ++i) {
+        if (rows[i] >= p.m) continue;
+        const int64_t o = rows[i] * p.n + col;
+        float v0 = dequant<BIAS>(acc[i][j][0], rsv[i], cs.x, b0);
+        float v1 = dequant<BIAS>(acc[i][j][1], rsv[i], cs.y, b1);
+        float v2 = dequant<BIAS>(acc[i][j][2], rsv[i], cs.z, b2);
+        float v3 = dequant<BIAS>(acc[i][j][3], rsv[i], cs.w, b3);
+        if (EPI == EPI_GATED) {
+          const uint2 xv = *reinterpret_cast<const uint2*>(p.resid + o);
+          const uint2 gv = *reinterpret_cast<const uint2*>(
+              p.table + trow[i] * p.table_width + (int64_t)p.gate_slot * p.n + col);
+          v0 = finish<EPI>(v0, bf_lo(gv.x), bf_lo(xv.x));
+          v1 = finish<EPI>(v1, bf_hi(gv.x), bf_hi(xv.x));
+          v2 = finish<EPI>(v2, bf_lo(gv.y), bf_lo(xv.y));
+          v3 = finish<EPI>(v3, bf_hi(gv.y), bf_hi(xv.y));
+        } else {
+          v0 = finish<EPI>(v0, 0.f, 0.f);
+          v1 = finish<EPI>(v1, 0.f, 0.f);
+          v2 = finish<EPI>(v2, 0.f, 0.f);
+          v3 = finish<EPI>(v3, 0.f, 0.f);
+        }
+        *reinterpret_cast<uint2*>(static_cast<uint16_t*>(p.c) + o) =
+            make_uint2(pack_bf2(v0, v1), pack_bf2(v2, v3));
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < FM; ++i) {
+        if (rows[i] >= p.m) continue;
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (col + e < p.n) store_scalar<EPI, BIAS>(p, rows[i], col + e, acc[i][j][e]);
+      }
+    }
+  }
+}
+
+// -------------------------------------------------------- generic GEMM ----
+// 64x64 tile per block, 4x4 outputs per thread, K in steps of 32 through LDS.
+template <int EPI, bool BIAS>
+__global__ __launch_bounds__(256) void gemm_generic(GemmArgs p) {
+  __shared__ int As[32][64 + 1];
+  __shared__ int Bs[32][64 + 1];
+  const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
+  const int64_t m0 = (int64_t)blockIdx.y * 64, n0 = (int64_t)blockIdx.x * 64;
+  int acc[4][4] = {};
+  for (int64_t k0 = 0; k0 < p.k; k0 += 32) {
+    for (int idx = threadIdx.x; idx < 64 * 32; idx += 256) {
+      const int r = idx >> 5, kk = idx & 31;
+      const int64_t gm = m0 + r, gk = k0 + kk;
+      As[kk][r] = (gm < p.m && gk < p.k) ? (int)p.a[gm * p.k + gk] : 0;
+      const int64_t gn = n0 + r;
+      Bs[kk][r] = (gn < p.n && gk < p.k) ? (int)p.b[gk * p.b_sk + gn * p.b_sn] : 0;
+    }
+    __syncthreads();
+#pragma unroll 4
+    for (int kk = 0; kk < 32; ++kk) {
+      int av[4], bv[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) av[i] = As[kk][ty * 4 + i];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) bv[j] = Bs[kk][tx * 4 + j];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] += av[i] * bv[j];
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int64_t row = m0 + ty * 4 + i, col = n0 + tx * 4 + j;
+      if (row < p.m && col < p.n) store_scalar<EPI, BIAS>(p, row, col, acc[i][j]);
+    }
+}
+
+// ------------------------------------------------------------- launch ----
+struct FastCfg {
+  int bm, bn;
+};
+
+template <int BM, int BN, int WAVES_M, int STAGES, int EPI, bool BIAS>
+void launch_fast_cfg(GemmArgs& p, hipStream_t st) {
+  p.tiles_m = (int)((p.m + BM - 1) / BM);
+  p.tiles_n = (int)((p.n + BN - 1) / BN);
+  const unsigned grid = (unsigned)(p.tiles_m * p.tiles_n);
+  hipLaunchKernelGGL((gemm_fast<BM, BN, WAVES_M, STAGES, EPI, BIAS>), dim3(grid), dim3(256), 0, st, p);
+}
+
+template <int EPI, bool BIAS>
+void launch_fast(int tile, GemmArgs& p, hipStream_t st) {
+  switch (tile) {
+    case LR_TILE_256x256: launch_fast_cfg<256, 256, 2, 4, EPI, BIAS>(p, st); break;
+    case LR_TILE_256x128: launch_fast_cfg<256, 128, 2, 4, EPI, BIAS>(p, st); break;
+    case LR_TILE_128x256: launch_fast_cfg<128, 256, 2, 4, EPI, BIAS>(p, st); break;
+    case LR_TILE_128x128: launch_fast_cfg<128, 128, 2, 4, EPI, BIAS>(p, st); break;
+    default: launch_fast_cfg<64, 128, 1, 4, EPI, BIAS>(p, st); break;
+  }
+}
+
+template <int EPI, bool BIAS>
+void launch_generic(GemmArgs& p, hipStream_t st) {
+  const dim3 grid((unsigned)((p.n + 63) / 64), (unsigned)((p.m + 63) / 64));
+  hipLaunchKernelGGL((gemm_generic<EPI, BIAS>), grid, dim3(256), 0, st, p);
+}
+
+template <int EPI>
+void dispatch_bias(bool generic, int tile, bool bias, GemmArgs& p, hipStream_t st) {
+  if (generic) {
+    if (bias) launch_generic<EPI, true>(p, st);
+    else launch_generic<EPI, false>(p, st);
+  } else {
+    if (bias) launch_fast<EPI, true>(tile, p, st);
+    else launch_fast<EPI, false>(tile, p, st);
+  }
+}
+
+int tile_rows(int tile) {
+  switch (tile) {
+    case LR_TILE_256x256: case LR_TILE_256x128: return 256;
+    case LR_TILE_128x256: case LR_TILE_128x128: return 128;
+    default: return 64;
+  }
+}
+int tile_cols(int tile) {
+  switch (tile) {
+    case LR_TILE_256x256: case LR_TILE_128x256: return 256;
+    default: return 128;
+  }
+}
+
+// Shape heuristic: the largest tile that still gives every CU work.
+int auto_tile(int64_t m, int64_t n) {
+  const int64_t cus = 256;
+  auto tiles = [&](int t) { return ((m + tile_rows(t) - 1) / tile_rows(t)) * ((n + tile_cols(t) - 1) / tile_cols(t)); };
+  if (tiles(LR_TILE_256x256) >= 2 * cus) return LR_TILE_256x256;
+  if (tiles(LR_TILE_256x128) >= 2 * cus) return LR_TILE_256x128;
+  if (tiles(LR_TILE_128x128) >= cus) return LR_TILE_128x128;
+  return LR_TILE_64x128;
+}
+
+}  // namespace
+}  // namespace lr
+
+using namespace lr;
+
+static int g_group_m_override = 0;
+
+extern "C" int lr_int8_gemm(const int8_t* a, const int8_t* b, int64_t b_stride_k,
+                            int64_t b_stride_n, int64_t m, int64_t n, int64_t k,
+                            const float* row_scale, const float* col_scale, const void* bias,
+                            void* c, int epilogue, const void* residual, const void* table,
+                            int64_t table_rows, int64_t table_width, const int64_t* indices,
+                            int64_t sequence, int gate_slot, int tile, void* stream) {
+  LR_REQUIRE(m >= 0 && n >= 0 && k >= 0, "int8_gemm: negative shape");
+  LR_REQUIRE(epilogue >= LR_EPI_BF16 && epilogue <= LR_EPI_RAW_INT32,
+             "int8_gemm: unknown epilogue %d", epilogue);
+  LR_REQUIRE(tile >= LR_TILE_AUTO && tile <= LR_TILE_GENERIC, "int8_gemm: unknown tile %d", tile);
+  if (m == 0 || n == 0) return LR_OK;
+  LR_REQUIRE(a && b && c, "int8_gemm: null A/B/C");
+  if (epilogue != LR_EPI_RAW_INT32) LR_REQUIRE(row_scale && col_scale, "int8_gemm: null scales");
+  if (epilogue == LR_EPI_GATED_RESIDUAL) {
+    LR_REQUIRE(residual && table && indices, "int8_gemm: gated residual needs residual/table/indices");
+    LR_REQUIRE(sequence > 0 && table_rows > 0 && gate_slot >= 0,
+               "int8_gemm: bad gated-residual sequence/table/slot");
+    LR_REQUIRE((int64_t)(gate_slot + 1) * n <= table_width,
+               "int8_gemm: table width %lld too small for gate slot %d", (long long)table_width,
+               gate_slot);
+  }
+  GemmArgs p{};
+  p.a = a; p.b = b; p.rs = row_scale; p.cs = col_scale; p.bias = (const uint16_t*)bias;
+  p.c = c; p.resid = (const uint16_t*)residual; p.table = (const uint16_t*)table;
+  p.indices = indices; p.m = m; p.n = n; p.k = k; p.b_sk = b_stride_k; p.b_sn = b_stride_n;
+  p.table_rows = table_rows; p.table_width = table_width; p.sequence = sequence;
+  p.gate_slot = gate_slot;
+  p.group_m = g_group_m_override > 0 ? g_group_m_override : 8;
+  p.nvec = n % 4 == 0 && aligned(c, epilogue == LR_EPI_RAW_INT32 ? 16 : 8) &&
+           (epilogue == LR_EPI_RAW_INT32 || aligned(col_scale, 16)) &&
+           (bias == nullptr || aligned(bias, 8)) &&
+           (epilogue != LR_EPI_GATED_RESIDUAL ||
+            (aligned(residual, 8) && aligned(table, 8) && table_width % 4 == 0));
+
+  // Fast path: W stored [N,K] row-major with 16-byte aligned rows; buffer
+  // descriptors need per-block ranges (256 rows * K) below 2^31 bytes.
+  const bool fast = b_stride_k == 1 && b_stride_n == k && k % 16 == 0 && k > 0 &&
+                    aligned(a, 16) && aligned(b, 16) && k <= (1LL << 22) &&
+                    tile != LR_TILE_GENERIC;
+  if (!fast) {
+    LR_REQUIRE((m + 63) / 64 <= 65535, "int8_gemm: generic path supports M <= 4194240");
+  } else {
+    if (tile == LR_TILE_AUTO) tile = auto_tile(m, n);
+    const int64_t tiles = ((m + tile_rows(tile) - 1) / tile_rows(tile)) *
+                          ((n + tile_cols(tile) - 1) / tile_cols(tile));
+    LR_REQUIRE(tiles <= 0x7fffffffLL, "int8_gemm: too many tiles");
+  }
+  hipStream_t st = as_stream(stream);
+  const bool has_bias = bias != nullptr && epilogue != LR_EPI_RAW_INT32;
+  switch (epilogue) {
+    case LR_EPI_BF16: dispatch_bias<EPI_BF16>(!fast, tile, has_bias, p, st); break;
+    case LR_EPI_GELU_TANH: dispatch_bias<EPI_GELU>(!fast, tile, has_bias, p, st); break;
+    case LR_EPI_GATED_RESIDUAL: dispatch_bias<EPI_GATED>(!fast, tile, has_bias, p, st); break;
+    default: dispatch_bias<EPI_RAW>(!fast, tile, false, p, st); break;
+  }
+  return check_launch("int8_gemm");
+}
+
+// Tuning hook: rows of tiles per raster group (0 = default 8).
+extern "C" int lr_gemm_set_group_m(int group_m) {
+  LR_REQUIRE(group_m >= 0 && group_m <= 64, "group_m out of range");
+  g_group_m_override = group_m;
+  return LR_OK;
+}

@@ -1,0 +1,198 @@
+"""Fused row/element-wise kernels of the W8A8 path, on gfx950 HIP.
+
+Same names, signatures and output allocation as the reference's Triton module
+model/kernels.py; each function launches one kernel of liblynnreal_amd.so on
+the caller's current stream. Outputs are allocated with torch.empty on the
+input's device (the reference's ownership rule); inputs are made contiguous
+and never modified.
+
+Arithmetic (all fp32 with the reference's bf16 rounding points):
+  quantize_rows        s = max(absmax, 1e-8)/127; q = clamp(rint(x/s), +-127)
+                       (the torch path, model/int8.py:66-67)
+  int8_epilogue        bf16((acc*as)*ws + bias)               kernels.py:27-38
+  _rms_adaln(_quant)   RMSNorm*gamma -> bf16, *bf16(1+scale) -> bf16,
+                       +shift -> bf16 (-> INT8)               kernels.py:48-128
+  residual_rms_quant   x' = bf16(x + bf16(gate2*u)), then slots 3/4
+                                                              kernels.py:405-419
+  _gated_residual      bf16(x + bf16(gate*u))                 kernels.py:131-153
+  _swiglu(_quant)      bf16(v * bf16(g*sigmoid(g))) (-> INT8)  kernels.py:156-185
+  gelu_tanh            bf16(gelu_tanh(x))  (new: the BASELINE FFN activation)
+
+The RMSNorm sum of squares uses one fixed reduction order (documented in
+include/lynnreal_amd.h) and an IEEE 1/sqrt, so the bf16 outputs reproduce a
+CPU restatement exactly; against the reference's Triton tree-sum and
+approximate rsqrt they agree to a bf16 ulp.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+
+
+def _bf16(t: torch.Tensor, what: str) -> torch.Tensor:
+    if t.dtype != torch.bfloat16:
+        raise ValueError(f"{what} must be bfloat16, got {t.dtype}")
+    return t.contiguous()
+
+
+def _norm_args(source, norm, table, indices):
+    source = _bf16(source, "source")
+    _lib.check_device(source)
+    weight = getattr(norm, "weight", None)
+    if weight is None:
+        raise ValueError("norm must have a weight")
+    weight = _bf16(weight, "norm.weight")
+    table = _bf16(table, "table")
+    indices = indices.reshape(-1).contiguous()
+    if indices.dtype != torch.int64:
+        indices = indices.to(torch.int64)
+    hidden = source.shape[-1]
+    sequence = source.shape[-2] if source.dim() >= 2 else 1
+    if weight.numel() != hidden:
+        raise ValueError(f"norm.weight has {weight.numel()} elements, expected {hidden}")
+    if indices.numel() < sequence:
+        raise ValueError(f"indices has {indices.numel()} entries for a sequence of {sequence}")
+    width = table.shape[-1]
+    table_rows = table.numel() // width if width else 0
+    return source, weight, table, indices, hidden, sequence, width, table_rows
+
+
+def quantize_rows(value):
+    """Per-row symmetric INT8 quantizer (model/kernels.py:19-24)."""
+    rows, width = value.shape
+    value = _bf16(value, "value")
+    _lib.check_device(value)
+    output = torch.empty_like(value, dtype=torch.int8)
+    scales = torch.empty(rows, 1, device=value.device, dtype=torch.float32)
+    _lib.call("lr_quantize_rows", value.data_ptr(), rows, width, output.data_ptr(),
+              scales.data_ptr(), _lib.stream(value))
+    return output, scales
+
+
+def int8_epilogue(accumulator, activation_scale, weight_scale, bias):
+    """INT32 -> bf16 dequant epilogue (model/kernels.py:41-46)."""
+    if accumulator.dtype != torch.int32:
+        raise ValueError("accumulator must be int32")
+    accumulator = accumulator.contiguous()
+    _lib.check_device(accumulator)
+    width = accumulator.shape[-1]
+    rows = accumulator.numel() // width if width else 0
+    a_scale = activation_scale.reshape(-1).float().contiguous()
+    w_scale = weight_scale.reshape(-1).float().contiguous()
+    if a_scale.numel() != rows or w_scale.numel() != width:
+        raise ValueError("scale shapes do not match the accumulator")
+    if bias is not None:
+        bias = _bf16(bias.reshape(-1), "bias")
+        if bias.numel() != width:
+            raise ValueError("bias shape does not match the accumulator")
+    output = torch.empty_like(accumulator, dtype=torch.bfloat16)
+    _lib.call("lr_int8_epilogue", accumulator.data_ptr(), a_scale.data_ptr(), w_scale.data_ptr(),
+              _lib.ptr(bias), output.data_ptr(), rows, width, _lib.stream(accumulator))
+    return output
+
+
+def _rms_adaln(source, norm, table, indices, shift_slot, scale_slot):
+    """RMSNorm + adaLN modulate, bf16 out (model/kernels.py:260-272)."""
+    source, weight, table, indices, hidden, sequence, width, table_rows = _norm_args(
+        source, norm, table, indices)
+    rows = source.numel() // hidden
+    output = torch.empty_like(source)
+    _lib.call("lr_rms_adaln", source.data_ptr(), weight.data_ptr(), table.data_ptr(),
+              indices.data_ptr(), output.data_ptr(), rows, sequence, hidden, table_rows, width,
+              int(shift_slot), int(scale_slot), float(norm.eps), _lib.stream(source))
+    return output
+
+
+def _rms_adaln_quant_int8(source, norm, table, indices, shift_slot, scale_slot):
+    """RMSNorm + adaLN modulate + INT8 quant (model/kernels.py:275-289)."""
+    source, weight, table, indices, hidden, sequence, width, table_rows = _norm_args(
+        source, norm, table, indices)
+    rows = source.numel() // hidden
+    output = torch.empty((rows, hidden), device=source.device, dtype=torch.int8)
+    scales = torch.empty((rows, 1), device=source.device, dtype=torch.float32)
+    _lib.call("lr_rms_adaln_quant", source.data_ptr(), weight.data_ptr(), table.data_ptr(),
+              indices.data_ptr(), output.data_ptr(), scales.data_ptr(), rows, sequence, hidden,
+              table_rows, width, int(shift_slot), int(scale_slot), float(norm.eps),
+              _lib.stream(source))
+    return output, scales
+
+
+def residual_rms_quant(source, update, norm, table, indices):
+    """Gated residual (slot 2) fused with norm/modulate (slots 3, 4) and INT8
+    quant (model/kernels.py:405-419)."""
+    source, weight, table, indices, hidden, sequence, width, table_rows = _norm_args(
+        source, norm, table, indices)
+    update = _bf16(update, "update")
+    if update.shape != source.shape:
+        raise ValueError("update must have the shape of source")
+    rows = source.numel() // hidden
+    residual = torch.empty_like(source)
+    quantized = torch.empty((rows, hidden), device=source.device, dtype=torch.int8)
+    scales = torch.empty((rows, 1), device=source.device, dtype=torch.float32)
+    _lib.call("lr_residual_rms_quant", source.data_ptr(), update.data_ptr(), weight.data_ptr(),
+              table.data_ptr(), indices.data_ptr(), residual.data_ptr(), quantized.data_ptr(),
+              scales.data_ptr(), rows, sequence, hidden, table_rows, width, float(norm.eps),
+              _lib.stream(source))
+    return residual, quantized, scales
+
+
+def _gated_residual(residual, update, table, indices, gate_slot):
+    """residual + gate * update with per-token gate (model/kernels.py:292-304)."""
+    residual = _bf16(residual, "residual")
+    _lib.check_device(residual)
+    update = _bf16(update, "update")
+    if update.shape != residual.shape:
+        raise ValueError("update must have the shape of residual")
+    table = _bf16(table, "table")
+    indices = indices.reshape(-1).contiguous()
+    if indices.dtype != torch.int64:
+        indices = indices.to(torch.int64)
+    hidden = residual.shape[-1]
+    sequence = residual.shape[-2] if residual.dim() >= 2 else 1
+    if indices.numel() < sequence:
+        raise ValueError(f"indices has {indices.numel()} entries for a sequence of {sequence}")
+    width = table.shape[-1]
+    rows = residual.numel() // hidden
+    output = torch.empty_like(residual)
+    _lib.call("lr_gated_residual", residual.data_ptr(), update.data_ptr(), table.data_ptr(),
+              indices.data_ptr(), output.data_ptr(), rows, sequence, hidden,
+              table.numel() // width if width else 0, width, int(gate_slot),
+              _lib.stream(residual))
+    return output
+
+
+def _swiglu(projected):
+    """SwiGLU of [.., 2I] -> [.., I] (model/kernels.py:307-315)."""
+    projected = _bf16(projected, "projected")
+    _lib.check_device(projected)
+    inner = projected.shape[-1] // 2
+    rows = projected.numel() // projected.shape[-1] if projected.shape[-1] else 0
+    output = torch.empty((*projected.shape[:-1], inner), device=projected.device,
+                         dtype=projected.dtype)
+    _lib.call("lr_swiglu", projected.data_ptr(), output.data_ptr(), rows, inner,
+              _lib.stream(projected))
+    return output
+
+
+def _swiglu_quant_int8(projected):
+    """SwiGLU + INT8 quant (model/kernels.py:318-328)."""
+    projected = _bf16(projected, "projected")
+    _lib.check_device(projected)
+    inner = projected.shape[-1] // 2
+    rows = projected.numel() // projected.shape[-1]
+    output = torch.empty((rows, inner), device=projected.device, dtype=torch.int8)
+    scales = torch.empty((rows, 1), device=projected.device, dtype=torch.float32)
+    _lib.call("lr_swiglu_quant", projected.data_ptr(), output.data_ptr(), scales.data_ptr(), rows,
+              inner, _lib.stream(projected))
+    return output, scales
+
+
+def gelu_tanh(value):
+    """Element-wise GELU (tanh approximation), bf16 in and out."""
+    value = _bf16(value, "value")
+    _lib.check_device(value)
+    output = torch.empty_like(value)
+    _lib.call("lr_gelu_tanh", value.data_ptr(), output.data_ptr(), value.numel(),
+              _lib.stream(value))
+    return output

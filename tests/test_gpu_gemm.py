@@ -1,0 +1,161 @@
+"""GPU parity of the INT8 MFMA GEMM (model/int8_gemm.py:13-46, :84-163).
+
+int32 accumulators bit-exact vs the oracle's int_mm; bf16 epilogue bit-exact
+vs the oracle's dequant (the reference asserts the same equality against its
+torch path, script/precompile.py:55-64); GELU-tanh within the bf16 tolerance;
+gated residual bit-exact vs the reference's _gated_residual composition.
+"""
+import hashlib
+
+import numpy as np
+import pytest
+import torch
+
+import golden_check
+import gpu_adapter as gpu
+from helpers import assert_bf16_close, bf16_randn, to_np
+from lynnreal_omni_amd import int8_gemm
+from oracle import reference as ref
+
+pytestmark = pytest.mark.gpu
+
+TILES = [None, (256, 256), (256, 128), (128, 256), (128, 128), (64, 128), "generic"]
+
+
+def gen(seed):
+    return torch.Generator().manual_seed(seed)
+
+
+def rand_i8(shape, g):
+    return torch.randint(-127, 128, shape, dtype=torch.int8, generator=g).numpy()
+
+
+@pytest.mark.parametrize("tile", TILES, ids=str)
+@pytest.mark.parametrize("m,n,k", [
+    (1, 64, 64), (7, 80, 48), (256, 256, 64), (300, 520, 272), (257, 255, 1024), (129, 384, 5120 + 16),
+])
+def test_int32_accumulators_bit_exact(m, n, k, tile):
+    g = gen(m * 7 + n * 3 + k)
+    a, w = rand_i8((m, k), g), rand_i8((n, k), g)
+    assert np.array_equal(gpu.int_mm(a, w, tile=tile), ref.int_mm(a, w))
+
+
+def test_extreme_values_reach_int32_range():
+    k = 20480
+    a = np.full((64, k), -127, np.int8)
+    w = np.full((128, k), -127, np.int8)
+    w[1::2] = 127
+    out = gpu.int_mm(a, w)
+    assert (out[:, 0::2] == 127 * 127 * k).all() and (out[:, 1::2] == -127 * 127 * k).all()
+
+
+def test_generic_paths_any_k_and_strides():
+    g = gen(11)
+    a, w = rand_i8((33, 100), g), rand_i8((70, 100), g)         # K % 16 != 0
+    assert np.array_equal(gpu.int_mm(a, w), ref.int_mm(a, w))
+    # B contiguous as [K, N] (strides (N, 1)): the generic kernel
+    at, bt = torch.from_numpy(a).cuda(), torch.from_numpy(np.ascontiguousarray(w.T)).cuda()
+    out = int8_gemm.int8_matmul_int32(at, bt)
+    torch.cuda.synchronize()
+    assert np.array_equal(out.cpu().numpy(), ref.int_mm(a, w))
+
+
+@pytest.mark.parametrize("tile", [None, (128, 128), "generic"], ids=str)
+@pytest.mark.parametrize("m,n,k,bias", [(45, 96, 256, True), (300, 1000, 640, False), (1, 8, 16, True)])
+def test_bf16_epilogue_bit_exact(m, n, k, bias, tile):
+    g = gen(m + n + k)
+    a, w = rand_i8((m, k), g), rand_i8((n, k), g)
+    rs = (torch.rand(m, generator=g) / 127).numpy()
+    cs = (torch.rand(n, generator=g) * 4e-3 + 1e-3).numpy()
+    b = to_np((torch.randn(n, generator=g) * 0.02).bfloat16()) if bias else None
+    y = gpu.linear(a, rs, w, cs, b, tile=tile)
+    assert np.array_equal(y, ref.linear(a, rs, w, cs, b))
+
+
+def test_gelu_epilogue_within_tolerance():
+    g = gen(12)
+    m, n, k = 200, 640, 512
+    a, w = rand_i8((m, k), g), rand_i8((n, k), g)
+    rs = (torch.rand(m, generator=g) / 127).numpy()
+    cs = (torch.rand(n, generator=g) * 4e-3 + 1e-3).numpy()
+    b = to_np((torch.randn(n, generator=g) * 0.02).bfloat16())
+    y = gpu.linear(a, rs, w, cs, b, activation="gelu_tanh")
+    expect = ref.gelu_tanh(ref.linear(a, rs, w, cs, b))
+    assert_bf16_close(y, expect, frac_exact=0.99, atol=1e-4)
+
+
+@pytest.mark.parametrize("tile", [None, (256, 256), "generic"], ids=str)
+def test_gated_residual_epilogue_bit_exact(tile):
+    g = gen(13)
+    batch, t, d, k = 2, 37, 320, 256
+    m = batch * t
+    a, w = rand_i8((m, k), g), rand_i8((d, k), g)
+    rs = (torch.rand(m, generator=g) / 127).numpy()
+    cs = (torch.rand(d, generator=g) * 4e-3 + 1e-3).numpy()
+    x = bf16_randn((batch, t, d), g)
+    table = bf16_randn((6, 6 * d), g, scale=0.1)
+    idx = torch.randint(0, 6, (t,), generator=g)
+    y = gpu.linear(a, rs, w, cs, None, tile=tile, residual=to_np(x), table=to_np(table),
+                   indices=idx.numpy(), gate_slot=5)
+    plain = ref.linear(a, rs, w, cs).reshape(batch, t, d)
+    expect = ref.gated_residual(to_np(x), plain, to_np(table), idx.numpy(), 5)
+    assert np.array_equal(y.reshape(batch, t, d), expect)
+
+
+@pytest.mark.parametrize("shape", list(golden_check.load_kat()), ids=str)
+def test_reference_install_check_shapes(shape):
+    """The reference's install-time shapes (script/precompile.py:50-64), digests
+    of the torch path's outputs committed in tests/golden/golden_kat.json."""
+    from golden.make_golden import kat_inputs
+    m, n, k = map(int, shape.split("x"))
+    a, w, rs, cs = kat_inputs(m, n, k)
+    want = golden_check.load_kat()[shape]
+    acc = gpu.int_mm(a.numpy(), w.numpy())
+    assert hashlib.sha256(acc.tobytes()).hexdigest() == want["acc_sha256"]
+    y = gpu.linear(a.numpy(), rs.numpy().reshape(-1), w.numpy(), cs.numpy().reshape(-1))
+    assert hashlib.sha256(y.tobytes()).hexdigest() == want["y_sha256"]
+
+
+def test_north_star_shape_sampled_rows():
+    """M=12288, K=5120, N=20480: the whole int32 product against torch's own
+    GPU int8 GEMM when it runs here, and sampled rows against the oracle."""
+    g = gen(14)
+    m, n, k = 12288, 20480, 5120
+    a = torch.randint(-127, 128, (m, k), dtype=torch.int8, generator=g).cuda()
+    w = torch.randint(-127, 128, (n, k), dtype=torch.int8, generator=g).cuda()
+    acc = int8_gemm.int8_matmul_int32(a, w.t())
+    rows = torch.cat([torch.arange(0, 64), torch.randint(64, m - 64, (64,), generator=g),
+                      torch.arange(m - 64, m)])
+    got = acc[rows.cuda()].cpu().numpy()
+    expect = ref.int_mm(a[rows.cuda()].cpu().numpy(), w.cpu().numpy())
+    assert np.array_equal(got, expect)
+    checksum_rows = acc.to(torch.int64).sum(dim=1).cpu()
+    # row sums by linearity: sum_n acc[m, n] = sum_k a[m, k] * (sum_n w[n, k])
+    expect_rows = (a.to(torch.int64) * w.to(torch.int64).sum(dim=0)).sum(dim=1).cpu()
+    assert torch.equal(checksum_rows, expect_rows)
+
+
+def test_torch_matmul_agrees_on_gpu():
+    """_torch_matmul (torch._int_mm on the GPU) and the MFMA kernel agree
+    bit for bit, as the reference's install check demands."""
+    g = gen(15)
+    m, n, k = 96, 320, 256
+    a = torch.randint(-127, 128, (m, k), dtype=torch.int8, generator=g).cuda()
+    b = torch.randint(-127, 128, (n, k), dtype=torch.int8, generator=g).cuda().t()
+    rs = (torch.rand(m, 1, generator=g) / 127).cuda()
+    cs = (torch.rand(1, n, generator=g) / 127).cuda()
+    try:
+        expect = int8_gemm._torch_matmul(a, b, rs, cs, None)
+    except RuntimeError as error:
+        pytest.skip(f"torch._int_mm unavailable on this GPU: {error}")
+    assert torch.equal(int8_gemm.int8_matmul(a, b, rs, cs), expect)
+
+
+def test_empty_and_invalid():
+    a = torch.zeros(0, 64, dtype=torch.int8, device="cuda")
+    b = torch.zeros(32, 64, dtype=torch.int8, device="cuda").t()
+    out = int8_gemm.int8_matmul(a, b, torch.ones(0, device="cuda"), torch.ones(32, device="cuda"))
+    assert out.shape == (0, 32)
+    with pytest.raises(ValueError):
+        int8_gemm.int8_matmul(torch.zeros(4, 64, dtype=torch.int8, device="cuda"), b,
+                              torch.ones(4, device="cuda"), torch.ones(31, device="cuda"))

@@ -1,0 +1,150 @@
+"""Host-side logic of the drop-in modules, on the CPU.
+
+Covers the reference-compatible surface that does not need a GPU: argument
+validation (model/int8_gemm.py:97-98, model/int8.py:29-30), tile mapping,
+Int8Linear's buffers and torch backend (model/int8.py:6-68), the converter
+(model/int8.py:71-104) and the error classifier (model/acceleration.py:49-56).
+"""
+import types
+
+import numpy as np
+import pytest
+import torch
+from torch import nn
+
+from helpers import bf16_randn, to_np
+from lynnreal_omni_amd import acceleration, int8_gemm, kernels
+from lynnreal_omni_amd.int8 import Int8Linear, quantize_transformer, quantize_weight
+from oracle import reference as ref
+
+
+def gen(seed):
+    return torch.Generator().manual_seed(seed)
+
+
+def test_tile_mapping():
+    assert int8_gemm._tile_id(None) == 0
+    assert int8_gemm._tile_id((128, 256, 128, 8, 3)) == 3
+    assert int8_gemm._tile_id((128, 256, 128, 8, 4, 8)) == 3
+    assert int8_gemm._tile_id((64, 128, 128, 4, 3, 0)) == 5
+    assert int8_gemm._tile_id("generic") == 6
+    for bad in ((32, 32, 64, 4, 2), (512, 512, 1, 1, 1), "fast", (1,)):
+        with pytest.raises(ValueError):
+            int8_gemm._tile_id(bad)
+
+
+def test_int8_matmul_validation():
+    a = torch.zeros(4, 8, dtype=torch.int8)
+    b = torch.zeros(8, 3, dtype=torch.int8)
+    rs, cs = torch.ones(4, 1), torch.ones(1, 3)
+    with pytest.raises(ValueError, match="contiguous row-major"):
+        int8_gemm.int8_matmul(a.float(), b, rs, cs)
+    with pytest.raises(ValueError, match="contiguous row-major"):
+        int8_gemm.int8_matmul(a.t(), b, rs, cs)
+    with pytest.raises(ValueError, match="contiguous row-major"):
+        int8_gemm.int8_matmul(a, b[:4], rs, cs)
+    with pytest.raises(ValueError, match="GPU tensors"):
+        int8_gemm.int8_matmul(a, b, rs, cs)
+
+
+def test_kernel_wrappers_validate_before_launch():
+    with pytest.raises(ValueError, match="bfloat16"):
+        kernels.quantize_rows(torch.zeros(2, 8))
+    with pytest.raises(ValueError, match="GPU tensors"):
+        kernels.quantize_rows(torch.zeros(2, 8, dtype=torch.bfloat16))
+    with pytest.raises(ValueError, match="int32"):
+        kernels.int8_epilogue(torch.zeros(2, 2), torch.ones(2), torch.ones(2), None)
+    norm = types.SimpleNamespace(weight=torch.ones(8, dtype=torch.float32), eps=1e-6)
+    with pytest.raises(ValueError, match="GPU tensors|bfloat16"):
+        kernels._rms_adaln(torch.zeros(1, 2, 8, dtype=torch.bfloat16), norm,
+                           torch.zeros(1, 48, dtype=torch.bfloat16), torch.zeros(2), 0, 1)
+
+
+def test_torch_matmul_matches_oracle():
+    g = gen(1)
+    a = torch.randint(-127, 128, (13, 64), dtype=torch.int8, generator=g)
+    w = torch.randint(-127, 128, (40, 64), dtype=torch.int8, generator=g)
+    rs = torch.rand(13, 1, generator=g) / 127
+    cs = torch.rand(1, 40, generator=g) / 127
+    bias = (torch.randn(40, generator=g) * 0.02).bfloat16()
+    y = int8_gemm._torch_matmul(a, w.t(), rs, cs, bias)
+    expect = ref.dequant(ref.int_mm(a.numpy(), w.numpy()), rs.numpy(), cs.numpy(), to_np(bias))
+    assert np.array_equal(to_np(y), expect)
+
+
+def test_int8_linear_buffers_and_torch_backend():
+    g = gen(2)
+    src = nn.Linear(96, 72, bias=True).to(torch.bfloat16)
+    with torch.no_grad():
+        src.weight.copy_(torch.randn(72, 96, generator=g).bfloat16())
+    layer = Int8Linear(src, gemm="torch")
+    assert layer.weight_int8.shape == (96, 72) and layer.weight_int8.stride() == (1, 96)
+    assert layer.weight_scale.shape == (1, 72) and layer.weight_scale.dtype == torch.float32
+    assert layer.bias.dtype == torch.bfloat16 and layer.weight.dtype == torch.bfloat16
+    assert layer.weight.numel() == 0
+    assert (layer.in_features, layer.out_features, layer.fused_ops) == (96, 72, False)
+    q, s = quantize_weight(src.weight)
+    assert torch.equal(layer.weight_int8.t(), q) and torch.equal(layer.weight_scale.t(), s)
+    x = bf16_randn((2, 5, 96), g, outliers=0.02)
+    y = layer(x)
+    assert y.shape == (2, 5, 72) and y.dtype == torch.bfloat16
+    qx, sx = ref.quantize_rows(to_np(x.reshape(-1, 96)))
+    expect = ref.linear(qx, sx, to_np(layer.weight_int8.t().contiguous()),
+                        layer.weight_scale.numpy(), to_np(layer.bias))
+    assert np.array_equal(to_np(y.reshape(-1, 72)), expect)
+    with pytest.raises(ValueError):
+        Int8Linear(src, gemm="cuda")
+
+
+def test_from_packed_keeps_rows_exactly():
+    g = gen(3)
+    w = torch.randint(-127, 128, (40, 24), dtype=torch.int8, generator=g)
+    s = torch.rand(40, 1, generator=g)
+    layer = Int8Linear.from_packed(w, s)
+    assert layer.gemm == "triton" and torch.equal(layer.weight_int8.t(), w)
+    assert layer.weight_scale.shape == (1, 40) and layer.weight.dtype == torch.bfloat16
+    with pytest.raises(ValueError, match="INT8"):
+        Int8Linear.from_packed(w.float(), s)
+    with pytest.raises(ValueError, match="INT8"):
+        Int8Linear.from_packed(w, s.t())
+
+
+def _fake_transformer(blocks=4, width=32, ffn=64):
+    def block():
+        attn = types.SimpleNamespace(
+            to_q=nn.Linear(width, width), to_k=nn.Linear(width, width, bias=False),
+            to_v=nn.Linear(width, width), to_out=[nn.Linear(width, width), nn.Identity()])
+        ff = types.SimpleNamespace(net=[types.SimpleNamespace(proj=nn.Linear(width, ffn)), None,
+                                        nn.Linear(ffn // 2, width)])
+        return types.SimpleNamespace(attn=attn, ff=ff)
+    return types.SimpleNamespace(transformer_blocks=[block() for _ in range(blocks)])
+
+
+def test_quantize_transformer():
+    t = _fake_transformer()
+    b1 = t.transformer_blocks[1]
+    q, k, v = b1.attn.to_q, b1.attn.to_k, b1.attn.to_v
+    report = quantize_transformer(t, protected_edges=1)
+    assert report["quantized_blocks"] == [1, 2] and report["quantized_linears"] == 8
+    for i, b in enumerate(t.transformer_blocks):
+        assert b.attn.to_q is None and b.attn.fused_projections
+        assert isinstance(b.attn.to_qkv, Int8Linear) == (i in (1, 2))
+    fused_w = torch.cat([q.weight, k.weight, v.weight])
+    wq, ws = quantize_weight(fused_w)
+    assert torch.equal(b1.attn.to_qkv.weight_int8.t(), wq)
+    bias = b1.attn.to_qkv.bias.float()
+    assert torch.equal(bias[32:64], torch.zeros(32))           # missing k bias -> zeros
+    assert torch.equal(bias[:32], q.bias.detach().bfloat16().float())
+    with pytest.raises(ValueError, match="unconverted"):
+        quantize_transformer(t)
+    with pytest.raises(ValueError, match="protected"):
+        quantize_transformer(_fake_transformer(blocks=2), protected_edges=1)
+
+
+def test_optional_kernel_failure():
+    ok = acceleration.optional_kernel_failure
+    assert ok(RuntimeError("lr_int8_gemm: int8_gemm: too many tiles (not supported)"))
+    assert ok(RuntimeError("no kernel image is available"))
+    assert not ok(RuntimeError("illegal memory access"))
+    assert not ok(ValueError("bad shape"))
+    assert not ok(torch.cuda.OutOfMemoryError("not supported"))
