@@ -45,9 +45,15 @@ def hipcc() -> str:
     return path
 
 
+# Per-file flags. The GEMM keeps at most 128 accumulators per wave and wants
+# them in VGPRs: with the default heuristic LLVM puts MFMA accumulators in
+# AGPRs and copies them between AGPRs and VGPRs inside the k-loop.
+FILE_FLAGS = {"gemm.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+
+
 def _compile(src: pathlib.Path, extra: list[str]) -> pathlib.Path:
     obj = OBJ / (src.stem + ".o")
-    cmd = [hipcc(), *FLAGS, *extra, "-c", str(src), "-o", str(obj)]
+    cmd = [hipcc(), *FLAGS, *FILE_FLAGS.get(src.name, []), *extra, "-c", str(src), "-o", str(obj)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"hipcc failed on {src.name}:\n{proc.stderr}")

@@ -6,15 +6,14 @@
 // plus GELU-tanh and gated-residual epilogues and a raw-int32 debug output.
 //
 // Fast kernel (A [M,K] row-major, W [N,K] row-major, K % 16 == 0):
-//  * Block tile BM x BN, K step 64, 256 threads = 4 waves in a WAVES_M x
-//    WAVES_N grid; each wave owns a (BM/WAVES_M) x (BN/WAVES_N) sub-tile made
-//    of 16x16 MFMA tiles (v_mfma_i32_16x16x64_i8), accumulators in AGPRs.
-//  * LDS holds STAGES k-steps. Each k-step of A (and of W) is stored as 1 KB
-//    "fragments" of 16 rows x 64 k, laid out in exactly the order the MFMA
-//    wants its operand: lane l's 16 bytes (row l%16, k 16*(l/16)..+15) sit at
-//    byte 16*l. A fragment is therefore read with one conflict-free
-//    ds_read_b128 per lane and written with one 16-byte-per-lane
-//    buffer_load ... lds (global -> LDS without touching VGPRs).
+//  * Block tile BM x BN, 4 or 8 waves in a WAVES_M x WAVES_N grid; each wave
+//    owns a (BM/WAVES_M) x (BN/WAVES_N) sub-tile of 16x16 MFMA tiles
+//    (v_mfma_i32_16x16x64_i8). At most 128 accumulators per wave, held in
+//    VGPRs (this file is compiled with -amdgpu-mfma-vgpr-form), so two waves
+//    share each SIMD and one wave's waits hide under the other's MFMAs.
+//  * Global -> LDS by buffer_load ... lds (16 bytes per lane, no VGPRs), in
+//    k-steps of 128 bytes so that each DMA reads whole 128-byte lines; LDS is
+//    double-buffered and XOR-swizzled for conflict-free ds_read_b128.
 //  * Buffer descriptors bound each block's rows, so rows past M/N and k past
 //    K read as zero: no masking in the main loop, tails are exact.
 //  * The MFMA is issued as W_frag x A_frag, so lane l ends with row l%16 and
@@ -119,36 +118,30 @@ __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t rsrc, void* lds, ui
   __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_ptr_t)lds, 16, voffset, 0, 0, 0);
 }
 
-__device__ __forceinline__ void wait_vmcnt(int n) {
-  // s_waitcnt with expcnt/lgkmcnt at their maximum: wait on vmcnt only.
-  // vmcnt is 6 bits on gfx9: [3:0] and [15:14].
-  switch (n) {
-#define LR_VM(N) \
-  case N: __builtin_amdgcn_s_waitcnt(((N) & 15) | (((N) >> 4) << 14) | 0x70 | 0xf00); break;
-    LR_VM(0) LR_VM(1) LR_VM(2) LR_VM(3) LR_VM(4) LR_VM(5) LR_VM(6) LR_VM(7) LR_VM(8)
-    LR_VM(9) LR_VM(10) LR_VM(11) LR_VM(12) LR_VM(13) LR_VM(14) LR_VM(15) LR_VM(16)
-    LR_VM(17) LR_VM(18) LR_VM(19) LR_VM(20) LR_VM(21) LR_VM(22) LR_VM(23) LR_VM(24)
-    LR_VM(25) LR_VM(26) LR_VM(27) LR_VM(28) LR_VM(29) LR_VM(30) LR_VM(31) LR_VM(32)
-#undef LR_VM
-    default: __builtin_amdgcn_s_waitcnt(0x70 | 0xf00); break;
-  }
-}
-
 // ----------------------------------------------------------- fast GEMM ----
-template <int BM, int BN, int WAVES_M, int STAGES, int EPI, bool BIAS>
-__global__ __launch_bounds__(256) void gemm_fast(GemmArgs p) {
-  constexpr int BK = 64;
-  constexpr int WAVES_N = 4 / WAVES_M;
+// K is consumed in k-steps of 128 bytes; two k-steps live in LDS (double
+// buffer). LDS image of one k-step of A (W is the same): 1 KB blocks of 8
+// rows x 128 bytes, written by one 16-byte-per-lane DMA each, so every DMA
+// reads 8 whole 128-byte lines (a 16-row x 64-byte shape runs the vector
+// memory path at a quarter of its rate). Within a row the eight 16-byte
+// chunks are stored XOR-swizzled: chunk c of row R sits in slot c ^ (R % 8).
+// For the MFMA read (lane l: row l % 16 of a 16-row fragment, chunk l / 16,
+// +4 for the second k64 half) each group of 8 lanes then reads 8 distinct
+// 16-byte bank groups; measured on gfx950 this runs ds_read_b128 at 94% of
+// the rate of a contiguous read (an extra (R / 8) % 2 term drops it to 71%).
+template <int BM, int BN, int WAVES_M, int WAVES_N, int EPI, bool BIAS>
+__global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_fast(GemmArgs p) {
+  constexpr int BK = 128;
+  constexpr int NWAVES = WAVES_M * WAVES_N;
   constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N;
   constexpr int FM = WM / 16, FN = WN / 16;
   constexpr int A_BYTES = BM * BK, B_BYTES = BN * BK;
   constexpr int STAGE_BYTES = A_BYTES + B_BYTES;
-  constexpr int A_LOADS = BM / 64, B_LOADS = BN / 64;  // 1 KB fragments per wave per k-step
-  constexpr int LOADS = A_LOADS + B_LOADS;
-  static_assert(WAVES_M * WAVES_N == 4, "4 waves");
-  static_assert(BM % 64 == 0 && BN % 64 == 0 && FM % 4 == 0 && FN >= 1, "tile shape");
-  static_assert(STAGES >= 3 && LOADS * (STAGES - 2) <= 32, "stages / vmcnt budget");
-  __shared__ __attribute__((aligned(1024))) char smem[STAGES * STAGE_BYTES];
+  constexpr int A_LOADS = BM / 8 / NWAVES, B_LOADS = BN / 8 / NWAVES;  // 1 KB DMAs per wave per k-step
+  static_assert(NWAVES == 4 || NWAVES == 8, "4 or 8 waves");
+  static_assert(A_LOADS * NWAVES * 8 == BM && B_LOADS * NWAVES * 8 == BN && A_LOADS >= 1 &&
+                    B_LOADS >= 1 && FM >= 1 && FN >= 1, "tile shape");
+  __shared__ __attribute__((aligned(1024))) char smem[2 * STAGE_BYTES];
 
   int tm, tn;
   tile_coords(p, tm, tn);
@@ -165,35 +158,48 @@ __global__ __launch_bounds__(256) void gemm_fast(GemmArgs p) {
   const __amdgpu_buffer_rsrc_t rb =
       __builtin_amdgcn_make_buffer_rsrc((void*)(p.b + n0 * K), (short)0, (int)(rows_b * K), 0x00020000);
 
-  const int kchunk = (lane >> 4) * 16;
+  // DMA lane mapping: block kb covers rows 8kb..8kb+7; lane l writes slot
+  // l % 8 of row 8kb + l / 8, which holds chunk (l % 8) ^ (l / 8).
+  const int drow = lane >> 3;
+  auto dma_chunk = [&](int) { return ((lane & 7) ^ drow) * 16; };
   uint32_t a_off[A_LOADS], b_off[B_LOADS];
+  int a_chk[A_LOADS], b_chk[B_LOADS];
 #pragma unroll
-  for (int i = 0; i < A_LOADS; ++i)
-    a_off[i] = (uint32_t)(((wave * A_LOADS + i) * 16 + (lane & 15)) * K + kchunk);
+  for (int i = 0; i < A_LOADS; ++i) {
+    const int kb = wave * A_LOADS + i;
+    a_chk[i] = dma_chunk(kb);
+    a_off[i] = (uint32_t)((kb * 8 + drow) * K + a_chk[i]);
+  }
 #pragma unroll
-  for (int j = 0; j < B_LOADS; ++j)
-    b_off[j] = (uint32_t)(((wave * B_LOADS + j) * 16 + (lane & 15)) * K + kchunk);
+  for (int j = 0; j < B_LOADS; ++j) {
+    const int kb = wave * B_LOADS + j;
+    b_chk[j] = dma_chunk(kb);
+    b_off[j] = (uint32_t)((kb * 8 + drow) * K + b_chk[j]);
+  }
 
   auto issue = [&](int kt, int stage) {
-    const bool kin = (int64_t)kt * BK + kchunk < K;
-    const uint32_t kofs = (uint32_t)kt * BK;
+    const int64_t kbase = (int64_t)kt * BK;
+    const uint32_t kofs = (uint32_t)kbase;
     char* sa = smem + stage * STAGE_BYTES;
     char* sb = sa + A_BYTES;
 #pragma unroll
     for (int i = 0; i < A_LOADS; ++i)
-      dma16(ra, sa + (wave * A_LOADS + i) * 1024, kin ? a_off[i] + kofs : 0x80000000u);
+      dma16(ra, sa + (wave * A_LOADS + i) * 1024,
+            kbase + a_chk[i] < K ? a_off[i] + kofs : 0x80000000u);
 #pragma unroll
     for (int j = 0; j < B_LOADS; ++j)
-      dma16(rb, sb + (wave * B_LOADS + j) * 1024, kin ? b_off[j] + kofs : 0x80000000u);
+      dma16(rb, sb + (wave * B_LOADS + j) * 1024,
+            kbase + b_chk[j] < K ? b_off[j] + kofs : 0x80000000u);
   };
 
-  auto read_a = [&](int kt, int i) -> v4i {
-    const char* sa = smem + (kt % STAGES) * STAGE_BYTES;
-    return *reinterpret_cast<const v4i*>(sa + (wm * FM + i) * 1024 + lane * 16);
-  };
-  auto read_w = [&](int kt, int j) -> v4i {
-    const char* sb = smem + (kt % STAGES) * STAGE_BYTES + A_BYTES;
-    return *reinterpret_cast<const v4i*>(sb + (wn * FN + j) * 1024 + lane * 16);
+  // Fragment read: 16-row fragment f spans blocks 2f, 2f+1.
+  const int r16 = lane & 15;
+  const int rd_key = r16 & 7;
+  const int rd_row = (r16 >> 3) * 1024 + (r16 & 7) * 128;
+  const int rd_slot0 = (((lane >> 4) + 0) ^ rd_key) * 16;
+  const int rd_slot1 = (((lane >> 4) + 4) ^ rd_key) * 16;
+  auto frag = [&](const char* base, int f, int h) -> v4i {
+    return *reinterpret_cast<const v4i*>(base + f * 2048 + rd_row + (h ? rd_slot1 : rd_slot0));
   };
 
   v4i acc[FM][FN];
@@ -202,61 +208,33 @@ __global__ __launch_bounds__(256) void gemm_fast(GemmArgs p) {
 #pragma unroll
     for (int j = 0; j < FN; ++j) acc[i][j] = v4i{0, 0, 0, 0};
 
-  // All waves wait for their own DMA of a k-step, then meet at the barrier:
-  // after it the k-step is complete in LDS, and every wave has finished the
-  // previous iteration (so the buffer it read may be overwritten).
-  auto sync_stage = [&](int pending_after) {
-    wait_vmcnt(pending_after * LOADS);
+  // Double buffer: wait for k-step kt's DMA, barrier (kt complete in LDS and
+  // every wave done with kt-1), start the DMA of kt+1 into the other buffer,
+  // then the MFMAs of kt with its fragments read from LDS. The two waves on
+  // each SIMD hide each other's LDS latency.
+  if (KT > 0) issue(0, 0);
+  for (int kt = 0; kt < KT; ++kt) {
+    __builtin_amdgcn_s_waitcnt(0x70 | 0xf00);  // vmcnt(0)
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
     __builtin_amdgcn_sched_barrier(0);
-  };
-
-  // Register schedule: W fragments are double-buffered per k-step (wf[parity]);
-  // A fragments rotate through 4 registers, read two MFMA rows ahead. During
-  // k-step kt the reads for k-step kt+1 (its first two A rows and all W
-  // fragments) are already issued, so the MFMA pipe never waits on LDS.
-  v4i wf[2][FN], af[4];
-
-  // Prologue: DMA k-steps 0 .. STAGES-2, then k-step 0's first fragments.
+    if (kt + 1 < KT) issue(kt + 1, (kt + 1) & 1);
+    const char* sa = smem + (kt & 1) * STAGE_BYTES;
+    const char* sb = sa + A_BYTES;
 #pragma unroll
-  for (int s = 0; s < STAGES - 1; ++s)
-    if (s < KT) issue(s, s);
-  if (KT > 0) {
-    sync_stage(min(STAGES - 2, KT - 1));
+    for (int h = 0; h < 2; ++h) {
+      v4i af[FM], wf[FN];
 #pragma unroll
-    for (int j = 0; j < FN; ++j) wf[0][j] = read_w(0, j);
-    af[0] = read_a(0, 0);
-    af[1] = read_a(0, 1);
+      for (int j = 0; j < FN; ++j) wf[j] = frag(sb, wn * FN + j, h);
+#pragma unroll
+      for (int i = 0; i < FM; ++i) af[i] = frag(sa, wm * FM + i, h);
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wf[j], af[i], acc[i][j], 0, 0, 0);
+    }
   }
-
-  // One k-step. next: a k-step kt+1 exists (sync it, prefetch its
-  // fragments); dma: k-step kt+STAGES-1 exists (start its DMA). Every call
-  // passes constants, so after inlining each phase below is branch-free.
-  auto step = [&](bool next, bool dma, int kt, int pending) __attribute__((always_inline)) {
-    if (next) sync_stage(pending);
-    if (dma) issue(kt + STAGES - 1, (kt + STAGES - 1) % STAGES);
-#pragma unroll
-    for (int i = 0; i < FM; ++i) {
-      const int r = i + 2;
-      if (r < FM) af[r % 4] = read_a(kt, r);
-      else if (next) af[r % 4] = read_a(kt + 1, r - FM);
-#pragma unroll
-      for (int j = 0; j < FN; ++j)
-        if (next && j * FM / FN == i) wf[1][j] = read_w(kt + 1, j);
-#pragma unroll
-      for (int j = 0; j < FN; ++j)
-        acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wf[0][j], af[i % 4], acc[i][j], 0, 0, 0);
-    }
-    if (next) {
-#pragma unroll
-      for (int j = 0; j < FN; ++j) wf[0][j] = wf[1][j];
-    }
-  };
-  int kt = 0;
-  for (; kt + STAGES - 1 < KT; ++kt) step(true, true, kt, STAGES - 3);  // steady state
-  for (; kt + 1 < KT; ++kt) step(true, false, kt, KT - 2 - kt);         // DMA drained
-  if (kt < KT) step(false, false, kt, 0);                               // last k-step
 
   // Epilogue. Lane l holds, for MFMA tile (i, j), row wm*WM + 16i + l%16 and
   // columns wn*WN + 16j + 4*(l/16) + 0..3.
@@ -375,21 +353,27 @@ struct FastCfg {
   int bm, bn;
 };
 
-template <int BM, int BN, int WAVES_M, int STAGES, int EPI, bool BIAS>
+template <int BM, int BN, int WAVES_M, int WAVES_N, int EPI, bool BIAS>
 void launch_fast_cfg(GemmArgs& p, hipStream_t st) {
   p.tiles_m = (int)((p.m + BM - 1) / BM);
   p.tiles_n = (int)((p.n + BN - 1) / BN);
   const unsigned grid = (unsigned)(p.tiles_m * p.tiles_n);
-  hipLaunchKernelGGL((gemm_fast<BM, BN, WAVES_M, STAGES, EPI, BIAS>), dim3(grid), dim3(256), 0, st, p);
+  hipLaunchKernelGGL((gemm_fast<BM, BN, WAVES_M, WAVES_N, EPI, BIAS>), dim3(grid),
+                     dim3(64 * WAVES_M * WAVES_N), 0, st, p);
 }
 
 template <int EPI, bool BIAS>
 void launch_fast(int tile, GemmArgs& p, hipStream_t st) {
   switch (tile) {
+    // 8 waves of 128x64; two 64 KB k-steps in LDS; 1 block per CU.
     case LR_TILE_256x256: launch_fast_cfg<256, 256, 2, 4, EPI, BIAS>(p, st); break;
-    case LR_TILE_256x128: launch_fast_cfg<256, 128, 2, 4, EPI, BIAS>(p, st); break;
-    case LR_TILE_128x256: launch_fast_cfg<128, 256, 2, 4, EPI, BIAS>(p, st); break;
-    case LR_TILE_128x128: launch_fast_cfg<128, 128, 2, 4, EPI, BIAS>(p, st); break;
+    // 8 waves of 64x128 (same block shape, other wave grid).
+    case LR_TILE_256x256_W4x2: launch_fast_cfg<256, 256, 4, 2, EPI, BIAS>(p, st); break;
+    // 4 waves of 128x64 / 64x128; two 48 KB k-steps.
+    case LR_TILE_256x128: launch_fast_cfg<256, 128, 2, 2, EPI, BIAS>(p, st); break;
+    case LR_TILE_128x256: launch_fast_cfg<128, 256, 2, 2, EPI, BIAS>(p, st); break;
+    // 4 waves of 64x64; two 32 KB k-steps: 2 blocks per CU.
+    case LR_TILE_128x128: launch_fast_cfg<128, 128, 2, 2, EPI, BIAS>(p, st); break;
     default: launch_fast_cfg<64, 128, 1, 4, EPI, BIAS>(p, st); break;
   }
 }
@@ -413,25 +397,26 @@ void dispatch_bias(bool generic, int tile, bool bias, GemmArgs& p, hipStream_t s
 
 int tile_rows(int tile) {
   switch (tile) {
-    case LR_TILE_256x256: case LR_TILE_256x128: return 256;
+    case LR_TILE_256x256: case LR_TILE_256x256_W4x2: case LR_TILE_256x128: return 256;
     case LR_TILE_128x256: case LR_TILE_128x128: return 128;
     default: return 64;
   }
 }
 int tile_cols(int tile) {
   switch (tile) {
-    case LR_TILE_256x256: case LR_TILE_128x256: return 256;
+    case LR_TILE_256x256: case LR_TILE_256x256_W4x2: case LR_TILE_128x256: return 256;
     default: return 128;
   }
 }
 
-// Shape heuristic: the largest tile that still gives every CU work.
+// Shape heuristic from measured sweeps on MI355X (256 CUs): the 8-wave
+// 256x256 tile (64x128 per wave) once there are two tiles per CU, 128x128
+// for medium grids, 64x128 for small M (decode-like, weight-bandwidth bound).
 int auto_tile(int64_t m, int64_t n) {
   const int64_t cus = 256;
   auto tiles = [&](int t) { return ((m + tile_rows(t) - 1) / tile_rows(t)) * ((n + tile_cols(t) - 1) / tile_cols(t)); };
-  if (tiles(LR_TILE_256x256) >= 2 * cus) return LR_TILE_256x256;
-  if (tiles(LR_TILE_256x128) >= 2 * cus) return LR_TILE_256x128;
-  if (tiles(LR_TILE_128x128) >= cus) return LR_TILE_128x128;
+  if (tiles(LR_TILE_256x256_W4x2) >= 2 * cus) return LR_TILE_256x256_W4x2;
+  if (tiles(LR_TILE_128x128) >= 4 * cus) return LR_TILE_128x128;
   return LR_TILE_64x128;
 }
 
@@ -451,7 +436,8 @@ extern "C" int lr_int8_gemm(const int8_t* a, const int8_t* b, int64_t b_stride_k
   LR_REQUIRE(m >= 0 && n >= 0 && k >= 0, "int8_gemm: negative shape");
   LR_REQUIRE(epilogue >= LR_EPI_BF16 && epilogue <= LR_EPI_RAW_INT32,
              "int8_gemm: unknown epilogue %d", epilogue);
-  LR_REQUIRE(tile >= LR_TILE_AUTO && tile <= LR_TILE_GENERIC, "int8_gemm: unknown tile %d", tile);
+  LR_REQUIRE(tile >= LR_TILE_AUTO && tile <= LR_TILE_256x256_W4x2, "int8_gemm: unknown tile %d",
+             tile);
   if (m == 0 || n == 0) return LR_OK;
   LR_REQUIRE(a && b && c, "int8_gemm: null A/B/C");
   if (epilogue != LR_EPI_RAW_INT32) LR_REQUIRE(row_scale && col_scale, "int8_gemm: null scales");
