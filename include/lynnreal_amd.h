@@ -123,8 +123,9 @@ int lr_rms_adaln(const void* x, const void* weight, const void* table, const int
  * y as in lr_rms_adaln, then q/scales as in lr_quantize_rows.
  * The sum of squares has one defined order so that results are reproducible:
  * the row is cut into 8-element chunks; chunk j is accumulated into slot
- * j % 256 (chunks in increasing j, elements in order, fp32); the 256 slots are
- * then combined by s[i] += s[i + h] for h = 128, 64, ..., 1. */
+ * j % 256 (chunks in increasing j, elements in order, s = fma(x, x, s) in
+ * fp32); the 256 slots are then combined by s[i] += s[i + h] for
+ * h = 128, 64, ..., 1. */
 int lr_rms_adaln_quant(const void* x, const void* weight, const void* table,
                        const int64_t* indices, int8_t* q, float* scales, int64_t rows,
                        int64_t sequence, int64_t hidden, int64_t table_rows, int64_t table_width,

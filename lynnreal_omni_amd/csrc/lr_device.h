@@ -29,6 +29,38 @@ __device__ __forceinline__ void store_nt(uint4* p, uint4 v) {
   __builtin_nontemporal_store(w, reinterpret_cast<v4u*>(p));
 }
 
+// Raw buffer access to one row of `bytes` bytes: loads past the end return
+// zero and stores past the end are dropped, so row tails need no branches.
+typedef unsigned v2u __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t row_rsrc(const void* base, int64_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
+                                           0x00020000);
+}
+// `voff` is the per-lane byte offset, `soff` a wave-uniform one (an SGPR or
+// constant, so that unrolled chunk loops share one offset register).
+// buf_load16 is for data read once (non-temporal); buf_load16_reused for data
+// that many waves read again (gamma, table rows).
+__device__ __forceinline__ uint4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t voff,
+                                            uint32_t soff = 0) {
+  const v4u v = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 2 /* nt */);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ uint4 buf_load16_reused(__amdgpu_buffer_rsrc_t r, uint32_t voff,
+                                                   uint32_t soff = 0) {
+  const v4u v = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ void buf_store16(__amdgpu_buffer_rsrc_t r, uint32_t voff,
+                                            uint32_t soff, uint4 v) {
+  const v4u w = {v.x, v.y, v.z, v.w};
+  __builtin_amdgcn_raw_buffer_store_b128(w, r, voff, soff, 0);
+}
+__device__ __forceinline__ void buf_store8(__amdgpu_buffer_rsrc_t r, uint32_t voff,
+                                           uint32_t soff, uint2 v) {
+  const v2u w = {v.x, v.y};
+  __builtin_amdgcn_raw_buffer_store_b64(w, r, voff, soff, 0);
+}
+
 // ---------------------------------------------------------------- bf16 ----
 __device__ __forceinline__ float bf_lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float bf_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
@@ -41,8 +73,30 @@ __device__ __forceinline__ uint32_t pack_bf2(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, b);
 }
 
-// float -> nearest bf16 -> float.
-__device__ __forceinline__ float round_bf(float x) { return bf_lo(pack_bf2(x, 0.0f)); }
+// float -> nearest bf16 -> float. One v_cvt_pk_bf16_f32 with a zero low half:
+// the packed word is then the rounded value's fp32 bit pattern.
+__device__ __forceinline__ float round_bf(float x) { return __uint_as_float(pack_bf2(0.0f, x)); }
+
+// Rounds two floats to bf16 with one instruction; returns the packed pair and
+// writes the rounded values back.
+__device__ __forceinline__ uint32_t round_bf2(float& a, float& b) {
+  const uint32_t r = pack_bf2(a, b);
+  a = bf_lo(r);
+  b = bf_hi(r);
+  return r;
+}
+
+__device__ __forceinline__ uint32_t word(const uint4& v, int i) {
+  return i == 0 ? v.x : (i == 1 ? v.y : (i == 2 ? v.z : v.w));
+}
+__device__ __forceinline__ void set_word(uint4& v, int i, uint32_t w) {
+  if (i == 0) v.x = w; else if (i == 1) v.y = w; else if (i == 2) v.z = w; else v.w = w;
+}
+
+// Hide a value from the optimizer's common-subexpression elimination (no code).
+__device__ __forceinline__ void opaque(uint4& v) {
+  asm volatile("" : "+v"(v.x), "+v"(v.y), "+v"(v.z), "+v"(v.w));
+}
 
 // Unpack 8 bf16 held in a uint4 into floats.
 __device__ __forceinline__ void unpack8(const uint4& v, float f[8]) {
@@ -67,35 +121,58 @@ __device__ __forceinline__ uint4 pack8(const float f[8]) {
 __device__ __forceinline__ float quant_scale(float absmax) { return fmaxf(absmax, 1e-8f) / 127.0f; }
 
 // q = clamp(rint_half_even(x / s), -127, 127) with x / s the IEEE fp32
-// quotient (model/int8.py:67). `inv` is the rounded reciprocal of s.
+// quotient (model/int8.py:67), for a bf16 value x of a row whose absmax gave
+// s = quant_scale(absmax), and inv = 1 / s (IEEE).
 //
-// With q = x/s exact and u = 2^-24: fl(1/s) = (1/s)(1+e1), y = fl(x*fl(1/s))
-// = q(1+e1)(1+e2) and fl(x/s) = q(1+e3), |ei| <= u, so
-// |y - fl(x/s)| <= 3u|q| <= 2.27e-5 because |x| <= absmax bounds |q| by
-// 127(1+2^-23). Unless y lies within 2^-14 (6.1e-5) of a half-integer, y and
-// fl(x/s) therefore round to the same integer. Inside that window (exact ties
-// are common among bf16 inputs) the IEEE quotient itself is rounded.
+// q0 = x * inv can differ from fl(x / s) by an ulp or two, enough to move a
+// result that lies on or next to a half-integer (exact ties are common among
+// bf16 inputs). One Markstein correction, r = fma(-q0, s, x) (exact) and
+// q1 = fma(r, inv, q0), removes that: rint(q1) equals the clamped
+// rint(fl(x / s)) for every bf16 absmax and every bf16 x with |x| <= absmax,
+// which tests/quant_division_check.c verifies exhaustively (about 10^9 pairs).
+// The clamp is therefore never active. Adding 1.5 * 2^23 rounds q1 to an
+// integer (half to even, as rint) and leaves it in the low bits of the sum,
+// whose low byte is the int8 two's complement. A NaN ends as 0.
+__device__ __forceinline__ uint32_t quant_bits(float x, float s, float inv) {
+  const float q0 = x * inv;
+  const float r = __builtin_fmaf(-q0, s, x);
+  const float q1 = __builtin_fmaf(r, inv, q0);
+  return __float_as_uint(q1 + 0x1.8p23f);
+}
+
 __device__ __forceinline__ int quant_one(float x, float s, float inv) {
-  float y = x * inv;
-  float n = __builtin_rintf(y);
-  if (__builtin_fabsf(y - n) >= 0.5f - 0x1p-14f) n = __builtin_rintf(x / s);
-  n = fminf(fmaxf(n, -127.0f), 127.0f);
-  return (int)n;
+  return (int)(int8_t)(quant_bits(x, s, inv) & 0xffu);
 }
 
-__device__ __forceinline__ uint32_t pack_i8x4(int a, int b, int c, int d) {
-  return (uint32_t)(a & 0xff) | ((uint32_t)(b & 0xff) << 8) | ((uint32_t)(c & 0xff) << 16) |
-         ((uint32_t)d << 24);
+// Low bytes of four words -> one word (three v_perm_b32).
+__device__ __forceinline__ uint32_t low_bytes4(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
+  const uint32_t ab = __builtin_amdgcn_perm(b, a, 0x0c0c0400u);
+  const uint32_t cd = __builtin_amdgcn_perm(d, c, 0x0c0c0400u);
+  return __builtin_amdgcn_perm(cd, ab, 0x05040100u);
 }
 
-// Quantize 8 values to 8 int8 packed in a uint2.
+// Quantize 8 values (bf16-exact floats) to 8 int8 packed in a uint2.
 __device__ __forceinline__ uint2 quant8(const float f[8], float s, float inv) {
-  uint2 r;
-  r.x = pack_i8x4(quant_one(f[0], s, inv), quant_one(f[1], s, inv), quant_one(f[2], s, inv),
-                  quant_one(f[3], s, inv));
-  r.y = pack_i8x4(quant_one(f[4], s, inv), quant_one(f[5], s, inv), quant_one(f[6], s, inv),
-                  quant_one(f[7], s, inv));
-  return r;
+  uint32_t t[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) t[e] = quant_bits(f[e], s, inv);
+  return make_uint2(low_bytes4(t[0], t[1], t[2], t[3]), low_bytes4(t[4], t[5], t[6], t[7]));
+}
+
+// Quantize the 8 bf16 of a uint4 to 8 int8 packed in a uint2.
+__device__ __forceinline__ uint2 quant8_bf(const uint4& v, float s, float inv) {
+  float f[8];
+  unpack8(v, f);
+  return quant8(f, s, inv);
+}
+
+// Max of |x| over the 8 bf16 of a uint4, folded into m.
+__device__ __forceinline__ float absmax8(const uint4& v, float m) {
+  m = fmaxf(fmaxf(m, __builtin_fabsf(bf_lo(v.x))), __builtin_fabsf(bf_hi(v.x)));
+  m = fmaxf(fmaxf(m, __builtin_fabsf(bf_lo(v.y))), __builtin_fabsf(bf_hi(v.y)));
+  m = fmaxf(fmaxf(m, __builtin_fabsf(bf_lo(v.z))), __builtin_fabsf(bf_hi(v.z)));
+  m = fmaxf(fmaxf(m, __builtin_fabsf(bf_lo(v.w))), __builtin_fabsf(bf_hi(v.w)));
+  return m;
 }
 
 // ------------------------------------------------------- activations ----
@@ -120,21 +197,49 @@ __device__ __forceinline__ float fast_gelu_tanh(float x) {
   return x * __builtin_amdgcn_rcpf(1.0f + e);
 }
 
-// ------------------------------------------------------- reductions ----
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+// Cross-lane partners without the LDS crossbar: lane l gets the value of
+// lane l ^ o. 32 and 16 use the gfx950 permlane swaps, whose two results hold
+// (v[l ^ o], v[l]) in some order, so only their sum or max is formed; 8 is a
+// rotation by 8 within a 16-lane row; 4 is a half-row mirror (l -> 7 - l)
+// followed by a quad reversal; 2 and 1 are quad permutations.
+template <int O>
+__device__ __forceinline__ float xor_partner(float v) {
+  const int u = __float_as_int(v);
+  if (O == 8) return __int_as_float(__builtin_amdgcn_mov_dpp(u, 0x128, 0xf, 0xf, false));
+  if (O == 4) {
+    const int m = __builtin_amdgcn_mov_dpp(u, 0x141, 0xf, 0xf, false);
+    return __int_as_float(__builtin_amdgcn_mov_dpp(m, 0x1b, 0xf, 0xf, false));
+  }
+  if (O == 2) return __int_as_float(__builtin_amdgcn_mov_dpp(u, 0x4e, 0xf, 0xf, false));
+  return __int_as_float(__builtin_amdgcn_mov_dpp(u, 0xb1, 0xf, 0xf, false));
+}
+
+template <bool MAX>
+__device__ __forceinline__ float wave_combine(float v) {
+  {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    const float a = __uint_as_float(r[0]), b = __uint_as_float(r[1]);
+    v = MAX ? fmaxf(a, b) : a + b;
+  }
+  {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    const float a = __uint_as_float(r[0]), b = __uint_as_float(r[1]);
+    v = MAX ? fmaxf(a, b) : a + b;
+  }
+  v = MAX ? fmaxf(v, xor_partner<8>(v)) : v + xor_partner<8>(v);
+  v = MAX ? fmaxf(v, xor_partner<4>(v)) : v + xor_partner<4>(v);
+  v = MAX ? fmaxf(v, xor_partner<2>(v)) : v + xor_partner<2>(v);
+  v = MAX ? fmaxf(v, xor_partner<1>(v)) : v + xor_partner<1>(v);
   return v;
 }
+
+// Max over the wave; every lane gets the result.
+__device__ __forceinline__ float wave_max(float v) { return wave_combine<true>(v); }
 
 // Butterfly sum over the wave: lane i adds lane i^o for o = 32..1. Because
 // float addition is commutative, every lane ends with the value the tree
 // s[i] += s[i+o] (i < o) leaves in s[0].
-__device__ __forceinline__ float wave_tree_sum(float v) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v = v + __shfl_xor(v, o, kWave);
-  return v;
-}
+__device__ __forceinline__ float wave_tree_sum(float v) { return wave_combine<false>(v); }
 
 // Block-wide max over 256 threads; every thread gets the result.
 __device__ __forceinline__ float block256_max(float v, float* red) {

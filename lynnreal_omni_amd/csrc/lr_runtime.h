@@ -22,6 +22,9 @@ inline int check_launch(const char* where) {
   return LR_OK;
 }
 
+// Compute units of the current device (cached per device; 256 if the query fails).
+int compute_units();
+
 inline bool aligned(const void* p, uintptr_t bytes) { return ((uintptr_t)p % bytes) == 0; }
 
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }

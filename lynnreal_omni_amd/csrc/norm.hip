@@ -2,18 +2,27 @@
 //
 // Restates model/kernels.py:48-128 (_rms_adaln_kernel and
 // _rms_adaln_quant_int8_kernel, incl. its WITH_RESIDUAL branch :101-105).
-// One 256-thread block owns one row (token). The row stays in registers from
-// the first read to the last write, so HBM sees each byte once:
+//
+// Main kernel: one wave per row (token), four rows per 256-thread block, no
+// block barriers. Lane l holds 16-byte chunks l, l+64, ... of the row in
+// registers from the first read to the last write, so HBM sees each byte once:
 //   rms_adaln            2 B in + 2 B out per element
 //   rms_adaln_quant      2 B in + 1 B out per element (+4 B/row)
 //   residual_rms_quant   4 B in + 3 B out per element (+4 B/row)
-// The gamma vector and the table rows are shared by all rows and stay in L2.
+// gamma and the table rows are shared by all rows and come from L2. The
+// arithmetic is VALU-bound at these byte counts, so bf16 roundings are done
+// two elements per v_cvt_pk_bf16_f32.
 //
 // The sum of squares uses one fixed order (8-element chunks, chunk j into
-// slot j % 256, then a pairwise tree over the 256 slots), so a CPU
-// restatement reproduces it bit for bit. The reference's Triton kernel sums
-// in its own tree order with an approximate rsqrt; against it the bf16
-// outputs agree to tolerance.
+// slot j % 256, slots combined by a pairwise tree; see lynnreal_amd.h), so a
+// CPU restatement reproduces it bit for bit. In the wave kernel lane l owns
+// slots l, l+64, l+128, l+192 (chunk l + 64m goes to slot l + 64(m % 4)); the
+// tree's two top levels are then lane-local and the rest is the butterfly.
+// The reference's Triton kernel sums in its own tree order with an
+// approximate rsqrt; against it the bf16 outputs agree to a bf16 ulp.
+//
+// Rows wider than the wave kernel holds (hidden > 8192) or unaligned rows use
+// a one-row-per-block kernel with the same arithmetic.
 #include "lr_device.h"
 #include "lr_runtime.h"
 
@@ -105,9 +114,9 @@ __global__ __launch_bounds__(kThreads) void rms_adaln_kernel(NormArgs p) {
         for (int e = 0; e < 8; ++e) v[i][e] = round_bf(v[i][e] + round_bf(gg[e] * uu[e]));
         store8<VEC>(p.resid_out + row * H, c, H, v[i]);
       }
-      // Each square of a bf16 is exact in fp32, so this is one rounding per add.
+      // A bf16 square is exact in fp32, so fma(x, x, s) is s + x*x rounded once.
 #pragma unroll
-      for (int e = 0; e < 8; ++e) acc = acc + v[i][e] * v[i][e];
+      for (int e = 0; e < 8; ++e) acc = __builtin_fmaf(v[i][e], v[i][e], acc);
     } else {
 #pragma unroll
       for (int e = 0; e < 8; ++e) v[i][e] = 0.0f;
@@ -154,8 +163,254 @@ __global__ __launch_bounds__(kThreads) void rms_adaln_kernel(NormArgs p) {
   }
 }
 
+// ------------------------------------------------ streaming kernel ----
+// A persistent grid (as many blocks as are resident) in which block
+// b owns rows [b * per_block, (b + 1) * per_block). At block start, gamma and
+// the modulation rows of the slice's first token are expanded into LDS as
+// fp32: gamma, bf16(1 + scale), shift and (residual) gate. Wave w of W then
+// streams rows start + w, start + w + W, ...: the next row's x (and u) loads are in
+// flight while the current row computes, and the current row reads its
+// parameters from LDS, whose waits (lgkmcnt) do not wait for those loads. A
+// row on a different table row reads its parameters from global memory.
+// Waves per block: 12 (three per SIMD) where the kernel fits in 168 VGPRs,
+// else 8. The LDS block is per block, so more waves per block share it.
+template <int CPL, bool RESID>
+constexpr int stream_waves() { return (RESID || CPL > 10) ? 8 : 12; }
+
+// LDS: parameter array a (0 gamma, 1 bf16(1 + scale), 2 shift, 3 gate),
+// chunk c, half h (elements 8c + 4h .. 8c + 4h + 3) at float4 (2a + h) * cap + c,
+// so that the 64 lanes of a wave read 64 consecutive float4s.
+template <int CPL, bool RESID>
+struct RowRegs {
+  uint4 x[CPL];
+  uint4 u[RESID ? CPL : 1];
+};
+
+template <int CPL, bool RESID>
+__device__ __forceinline__ void load_row(const NormArgs& p, int64_t row, RowRegs<CPL, RESID>& r) {
+  const int lane = threadIdx.x & 63;
+  const auto xr = row_rsrc(p.x + row * p.hidden, 2 * p.hidden);
+#pragma unroll
+  for (int m = 0; m < CPL; ++m) r.x[m] = buf_load16(xr, 16u * lane, 1024u * m);
+  if (RESID) {
+    const auto ur = row_rsrc(p.u + row * p.hidden, 2 * p.hidden);
+#pragma unroll
+    for (int m = 0; m < CPL; ++m) r.u[m] = buf_load16(ur, 16u * lane, 1024u * m);
+  }
+}
+
+// The 8 fp32 parameters of array a for chunk c, from LDS or from the table
+// row `trow` in global memory. Past the row end gamma, shift and gate read as
+// 0 and bf16(1 + scale) as 1, which keeps those lanes' outputs at zero.
+template <bool FROM_LDS>
+__device__ __forceinline__ void params8(const NormArgs& p, const uint16_t* trow,
+                                        const float4* lds, int cap, int a, int c, float f[8]) {
+  if (FROM_LDS) {
+    const float4 lo = lds[(2 * a) * cap + c], hi = lds[(2 * a + 1) * cap + c];
+    f[0] = lo.x; f[1] = lo.y; f[2] = lo.z; f[3] = lo.w;
+    f[4] = hi.x; f[5] = hi.y; f[6] = hi.z; f[7] = hi.w;
+  } else {
+    const uint16_t* src = a == 0 ? p.w
+                        : trow + (int64_t)(a == 1 ? p.scale_slot : (a == 2 ? p.shift_slot : 2)) *
+                                     p.hidden;
+    unpack8(buf_load16_reused(row_rsrc(src, 2 * p.hidden), 16u * (c & 63), 16u * (c & ~63)), f);
+    if (a == 1) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) f[e] = round_bf(1.0f + f[e]);
+    }
+  }
+}
+
+// Lanes past the row end hold zeros throughout (x and u read as zero, and
+// the parameters keep them there), so they add nothing to the sums and maxima,
+// and their stores fall outside the row's buffer range.
+template <int CPL, bool RESID, bool QUANT, bool FROM_LDS>
+__device__ __forceinline__ void norm_row(const NormArgs& p, int64_t row, const uint16_t* trow,
+                                         const float4* lds, RowRegs<CPL, RESID>& r) {
+  constexpr int cap = 64 * CPL;
+  const int lane = threadIdx.x & 63;
+  const int64_t H = p.hidden;
+  if (RESID) {
+    // x' = bf16(x + bf16(gate * u)), gate = table slot 2 (kernels.py:101-105)
+    const auto orow = row_rsrc(p.resid_out + row * H, 2 * H);
+#pragma unroll
+    for (int m = 0; m < CPL; ++m) {
+      const int c = lane + 64 * m;
+      float g[8], xf[8], uf[8];
+      params8<FROM_LDS>(p, trow, lds, cap, 3, c, g);
+      unpack8(r.x[m], xf);
+      unpack8(r.u[m], uf);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) xf[e] = xf[e] + round_bf(g[e] * uf[e]);
+      r.x[m] = pack8(xf);
+      buf_store16(orow, 16u * lane, 1024u * m, r.x[m]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+  // Lane l's slots l + 64k accumulate chunks m = k, k+4, k+8, ... in order.
+  // A bf16 square is exact in fp32, so fma(x, x, s) is s + x*x rounded once.
+  float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int m = 0; m < CPL; ++m) {
+    float f[8];
+    unpack8(r.x[m], f);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[m & 3] = __builtin_fmaf(f[e], f[e], acc[m & 3]);
+  }
+  const float ss = wave_tree_sum((acc[0] + acc[2]) + (acc[1] + acc[3]));
+  float ms = ss / (float)H;
+  ms = ms + p.eps;
+  const float rr = 1.0f / __builtin_sqrtf(ms);
+  // Keep the row packed across the reduction: unpacking it again below costs
+  // one instruction per element, holding it unpacked doubles the registers.
+#pragma unroll
+  for (int m = 0; m < CPL; ++m) opaque(r.x[m]);
+
+  // Chunk by chunk, with chunk m + 1's parameters read while chunk m computes;
+  // the scheduling barriers keep the compiler from hoisting every chunk's reads
+  // (which would need 24 registers per chunk).
+  const auto orow = row_rsrc(p.out + row * H, 2 * H);
+  float amax = 0.0f;
+  float nw[8], nmod[8], nsh[8];
+  params8<FROM_LDS>(p, trow, lds, cap, 0, lane, nw);
+  params8<FROM_LDS>(p, trow, lds, cap, 1, lane, nmod);
+  params8<FROM_LDS>(p, trow, lds, cap, 2, lane, nsh);
+#pragma unroll
+  for (int m = 0; m < CPL; ++m) {
+    const int c = lane + 64 * m;
+    float w[8], mod[8], sh[8], xf[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) w[e] = nw[e], mod[e] = nmod[e], sh[e] = nsh[e];
+    if (m + 1 < CPL) {
+      params8<FROM_LDS>(p, trow, lds, cap, 0, c + 64, nw);
+      params8<FROM_LDS>(p, trow, lds, cap, 1, c + 64, nmod);
+      params8<FROM_LDS>(p, trow, lds, cap, 2, c + 64, nsh);
+    }
+    unpack8(r.x[m], xf);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float n = round_bf((xf[e] * rr) * w[e]);
+      const float t = round_bf(n * mod[e]);
+      xf[e] = t + sh[e];
+      // bf16 rounding is monotonic and odd, so max |bf16(y)| = bf16(max |y|).
+      amax = fmaxf(amax, __builtin_fabsf(xf[e]));
+    }
+    r.x[m] = pack8(xf);
+    if (!QUANT) buf_store16(orow, 16u * lane, 1024u * m, r.x[m]);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  if (QUANT) {
+#pragma unroll
+    for (int m = 0; m < CPL; ++m) opaque(r.x[m]);  // as above, for y
+    const float s = quant_scale(wave_max(round_bf(amax)));
+    const float inv = 1.0f / s;
+    const auto qrow = row_rsrc(p.q + row * H, H);
+#pragma unroll
+    for (int m = 0; m < CPL; ++m) {
+      buf_store8(qrow, 8u * lane, 512u * m, quant8_bf(r.x[m], s, inv));
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if (lane == 0) p.scales[row] = s;
+  }
+}
+
+template <int CPL, bool RESID, bool QUANT>
+__global__ __launch_bounds__((64 * stream_waves<CPL, RESID>())) void rms_adaln_stream(
+    NormArgs p, int64_t rows, int64_t per_block) {
+  constexpr int kStreamWaves = stream_waves<CPL, RESID>();
+  constexpr int kStreamThreads = 64 * kStreamWaves;
+  constexpr int cap = 64 * CPL;
+  __shared__ float4 lds[(RESID ? 8 : 6) * cap];
+  const int64_t start = (int64_t)blockIdx.x * per_block;
+  const int64_t end = start + per_block < rows ? start + per_block : rows;
+  const int64_t tr_lds = clamp_index(p.indices[start % p.sequence], p.table_rows);
+  const uint16_t* trow = p.table + tr_lds * p.table_width;
+  for (int c = threadIdx.x; c < cap; c += kStreamThreads) {
+    const int na = RESID ? 4 : 3;
+    for (int a = 0; a < na; ++a) {
+      float f[8];
+      params8<false>(p, trow, nullptr, cap, a, c, f);
+      lds[(2 * a) * cap + c] = make_float4(f[0], f[1], f[2], f[3]);
+      lds[(2 * a + 1) * cap + c] = make_float4(f[4], f[5], f[6], f[7]);
+    }
+  }
+  // Does every row of the slice use the staged table row?
+  int same = 1;
+  for (int64_t r = start + threadIdx.x; r < end; r += kStreamThreads)
+    same &= clamp_index(p.indices[r % p.sequence], p.table_rows) == tr_lds;
+  same = __syncthreads_and(same);
+
+  const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  int64_t row = start + wave;
+  if (!same) {
+    // Mixed table rows: parameters from global memory, one row at a time.
+    RowRegs<CPL, RESID> rg;
+    for (; row < end; row += kStreamWaves) {
+      load_row(p, row, rg);
+      const int64_t tr = clamp_index(p.indices[row % p.sequence], p.table_rows);
+      norm_row<CPL, RESID, QUANT, false>(p, row, p.table + tr * p.table_width, nullptr, rg);
+    }
+    return;
+  }
+  RowRegs<CPL, RESID> ra, rb;
+  if (row < end) load_row(p, row, ra);
+  while (row < end) {
+    const int64_t next = row + kStreamWaves;
+    if (next < end) load_row(p, next, rb);
+    norm_row<CPL, RESID, QUANT, true>(p, row, nullptr, lds, ra);
+    row = next;
+    if (row >= end) break;
+    const int64_t after = row + kStreamWaves;
+    if (after < end) load_row(p, after, ra);
+    norm_row<CPL, RESID, QUANT, true>(p, row, nullptr, lds, rb);
+    row = after;
+  }
+}
+
+template <int CPL, bool RESID, bool QUANT>
+void launch_stream(const NormArgs& p, int64_t rows, hipStream_t st) {
+  constexpr int kStreamWaves = stream_waves<CPL, RESID>();
+  constexpr int kStreamThreads = 64 * kStreamWaves;
+  const auto kernel = rms_adaln_stream<CPL, RESID, QUANT>;
+  static int resident = 0;  // blocks per CU; the same for every gfx950 device
+  if (resident == 0) {
+    int nb = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, reinterpret_cast<const void*>(kernel),
+                                                     kStreamThreads, 0) != hipSuccess || nb < 1) {
+      (void)hipGetLastError();
+      nb = 1;
+    }
+    resident = nb;
+  }
+  const int64_t slots = (int64_t)compute_units() * resident;
+  int64_t per_block = (rows + slots - 1) / slots;
+  per_block = (per_block + kStreamWaves - 1) / kStreamWaves * kStreamWaves;
+  const int64_t grid = (rows + per_block - 1) / per_block;
+  hipLaunchKernelGGL(kernel, dim3((unsigned)grid), dim3(kStreamThreads), 0, st, p, rows,
+                     per_block);
+}
+
+// Rows up to 5120 wide (8192 without quantization) stay in registers without
+// spilling; wider rows take the one-row-per-block kernel.
+template <bool RESID, bool QUANT>
+bool launch_norm_stream(const NormArgs& p, int64_t rows, hipStream_t st) {
+  const int64_t need = (p.hidden / 8 + 63) / 64;
+  if (need <= 1) launch_stream<1, RESID, QUANT>(p, rows, st);
+  else if (need <= 2) launch_stream<2, RESID, QUANT>(p, rows, st);
+  else if (need <= 4) launch_stream<4, RESID, QUANT>(p, rows, st);
+  else if (need <= 6) launch_stream<6, RESID, QUANT>(p, rows, st);
+  else if (need <= 8) launch_stream<8, RESID, QUANT>(p, rows, st);
+  else if (need <= 10) launch_stream<10, RESID, QUANT>(p, rows, st);
+  else if (QUANT) return false;
+  else if (need <= 12) launch_stream<12, false, false>(p, rows, st);
+  else if (need <= 16) launch_stream<16, false, false>(p, rows, st);
+  else return false;
+  return true;
+}
+
 template <bool RESID, bool QUANT>
 int launch_norm(const NormArgs& p, int64_t rows, bool vec, hipStream_t st) {
+  if (vec && launch_norm_stream<RESID, QUANT>(p, rows, st)) return check_launch("rms_adaln");
   const int64_t chunks = (p.hidden + 7) / 8;
   const int64_t need = (chunks + kThreads - 1) / kThreads;
   if (need > 16)

@@ -2,11 +2,12 @@
 // INT32 -> bf16 dequant epilogue.
 //
 // quantize_rows restates model/int8.py:66-67 (the torch path; the Triton
-// kernel model/kernels.py:8-16 computes the same values). One 256-thread block
-// owns one row: the row is read once with 16-byte loads into registers,
-// reduced to its absmax with wave shuffles, then quantized from registers and
-// written with 8-byte stores. HBM traffic is the algorithmic 3 bytes/element
-// plus 4 bytes/row.
+// kernel model/kernels.py:8-16 computes the same values). Rows up to 8192
+// wide: one wave per row, four rows per 256-thread block; lane l holds 16-byte
+// chunks l, l+64, ... in registers, the absmax is a wave butterfly, and the
+// row is quantized from registers and written with 8-byte stores. Wider rows:
+// one 256-thread block per row, same scheme with a block reduction. HBM
+// traffic is the algorithmic 3 bytes/element plus 4 bytes/row.
 #include "lr_device.h"
 #include "lr_runtime.h"
 
@@ -14,6 +15,33 @@ namespace lr {
 namespace {
 
 constexpr int kThreads = 256;
+
+template <int CPL>
+__global__ __launch_bounds__(kThreads) void quantize_rows_wave(const uint4* __restrict__ x,
+                                                               uint2* __restrict__ q,
+                                                               float* __restrict__ scales,
+                                                               int64_t rows, int chunks) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = __builtin_amdgcn_readfirstlane((int)(blockIdx.x * 4 + (threadIdx.x >> 6)));
+  if (row >= rows) return;  // whole wave
+  // Buffer accesses: past the row end loads give zero and stores are dropped.
+  const auto src = row_rsrc(x + row * chunks, 16 * (int64_t)chunks);
+  const auto dst = row_rsrc(q + row * chunks, 8 * (int64_t)chunks);
+  uint4 v[CPL];
+  float m = 0.0f;
+#pragma unroll
+  for (int i = 0; i < CPL; ++i) v[i] = buf_load16(src, 16u * lane, 1024u * i);
+#pragma unroll
+  for (int i = 0; i < CPL; ++i) m = absmax8(v[i], m);
+  const float s = quant_scale(wave_max(m));
+  const float inv = 1.0f / s;
+#pragma unroll
+  for (int i = 0; i < CPL; ++i) {
+    buf_store8(dst, 8u * lane, 512u * i, quant8_bf(v[i], s, inv));
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  if (lane == 0) scales[row] = s;
+}
 
 template <int CPT>
 __global__ __launch_bounds__(kThreads) void quantize_rows_vec(const uint4* __restrict__ x,
@@ -24,24 +52,22 @@ __global__ __launch_bounds__(kThreads) void quantize_rows_vec(const uint4* __res
   const int64_t row = blockIdx.x;
   const uint4* src = x + row * chunks;
   uint2* dst = q + row * chunks;
-  float f[CPT][8];
+  uint4 v[CPT];
   float m = 0.0f;
 #pragma unroll
   for (int i = 0; i < CPT; ++i) {
     const int c = threadIdx.x + i * kThreads;
-    uint4 v = make_uint4(0, 0, 0, 0);
-    if (c < chunks) v = load_nt(src + c);
-    unpack8(v, f[i]);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) m = fmaxf(m, __builtin_fabsf(f[i][e]));
+    v[i] = c < chunks ? load_nt(src + c) : make_uint4(0, 0, 0, 0);
   }
+#pragma unroll
+  for (int i = 0; i < CPT; ++i) m = absmax8(v[i], m);
   m = block256_max(m, red);
   const float s = quant_scale(m);
   const float inv = 1.0f / s;
 #pragma unroll
   for (int i = 0; i < CPT; ++i) {
     const int c = threadIdx.x + i * kThreads;
-    if (c < chunks) dst[c] = quant8(f[i], s, inv);
+    if (c < chunks) dst[c] = quant8_bf(v[i], s, inv);
   }
   if (threadIdx.x == 0) scales[row] = s;
 }
@@ -69,6 +95,13 @@ void launch_quant_vec(const void* x, int8_t* q, float* s, int64_t rows, int chun
                       hipStream_t st) {
   hipLaunchKernelGGL(quantize_rows_vec<CPT>, dim3((unsigned)rows), dim3(kThreads), 0, st,
                      (const uint4*)x, (uint2*)q, s, chunks);
+}
+
+template <int CPL>
+void launch_quant_wave(const void* x, int8_t* q, float* s, int64_t rows, int chunks,
+                       hipStream_t st) {
+  hipLaunchKernelGGL(quantize_rows_wave<CPL>, dim3((unsigned)((rows + 3) / 4)), dim3(kThreads), 0,
+                     st, (const uint4*)x, (uint2*)q, s, rows, chunks);
 }
 
 // ------------------------------------------------------------ epilogue ----
@@ -127,7 +160,19 @@ extern "C" int lr_quantize_rows(const void* x, int64_t rows, int64_t width, int8
   const int64_t chunks = width / 8;
   const bool vec = width % 8 == 0 && aligned(x, 16) && aligned(q, 8) && chunks <= 16 * kThreads &&
                    width > 0;
-  if (vec) {
+  if (vec && chunks <= 16 * 64) {
+    const int need = (int)((chunks + 63) / 64);
+    const int c = (int)chunks;
+    if (need <= 1) launch_quant_wave<1>(x, q, scales, rows, c, st);
+    else if (need <= 2) launch_quant_wave<2>(x, q, scales, rows, c, st);
+    else if (need <= 3) launch_quant_wave<3>(x, q, scales, rows, c, st);
+    else if (need <= 4) launch_quant_wave<4>(x, q, scales, rows, c, st);
+    else if (need <= 6) launch_quant_wave<6>(x, q, scales, rows, c, st);
+    else if (need <= 8) launch_quant_wave<8>(x, q, scales, rows, c, st);
+    else if (need <= 10) launch_quant_wave<10>(x, q, scales, rows, c, st);
+    else if (need <= 12) launch_quant_wave<12>(x, q, scales, rows, c, st);
+    else launch_quant_wave<16>(x, q, scales, rows, c, st);
+  } else if (vec) {
     const int need = (int)((chunks + kThreads - 1) / kThreads);
     const int c = (int)chunks;
     if (need <= 1) launch_quant_vec<1>(x, q, scales, rows, c, st);

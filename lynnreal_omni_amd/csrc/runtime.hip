@@ -3,6 +3,8 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <atomic>
+
 #include "lr_runtime.h"
 
 namespace lr {
@@ -22,6 +24,23 @@ int hip_fail(hipError_t err, const char* where) {
   (void)hipGetLastError();
   return fail(err == hipErrorOutOfMemory ? LR_ENOMEM : LR_EHIP, "%s: %s (hip error %d)", where,
               hipGetErrorString(err), (int)err);
+}
+
+int compute_units() {
+  static std::atomic<int> cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+    (void)hipGetLastError();
+    return 256;
+  }
+  int n = cache[dev].load(std::memory_order_relaxed);
+  if (n > 0) return n;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) {
+    (void)hipGetLastError();
+    n = 256;
+  }
+  cache[dev].store(n, std::memory_order_relaxed);
+  return n;
 }
 
 }  // namespace lr

@@ -188,15 +188,16 @@ void lro_gated_residual(const uint16_t* x, const uint16_t* u, const uint16_t* ta
 /* ------------------------------------- RMSNorm + adaLN (+ quant) --- */
 /* Sum of squares in the order defined for the fused norm kernels: chunk j
  * (elements 8j .. 8j+7) goes to slot j % 256, each slot accumulates its
- * chunks in increasing j in fp32, and the 256 slots are combined by
- * s[i] += s[i + h] for h = 128, 64, ..., 1. */
+ * chunks in increasing j in fp32 as s = fmaf(x, x, s) (the square of a bf16
+ * is exact in fp32 unless |x| < 2^-67, so this is s + x*x rounded once), and
+ * the 256 slots are combined by s[i] += s[i + h] for h = 128, 64, ..., 1. */
 static float canonical_sumsq(const float* v, int64_t hidden) {
   float slot[256];
   for (int i = 0; i < 256; ++i) slot[i] = 0.0f;
   const int64_t chunks = (hidden + 7) / 8;
   for (int64_t j = 0; j < chunks; ++j) {
     float acc = slot[j % 256];
-    for (int64_t e = 8 * j; e < 8 * j + 8 && e < hidden; ++e) acc = acc + v[e] * v[e];
+    for (int64_t e = 8 * j; e < 8 * j + 8 && e < hidden; ++e) acc = fmaf(v[e], v[e], acc);
     slot[j % 256] = acc;
   }
   for (int h = 128; h >= 1; h >>= 1)
