@@ -26,6 +26,13 @@
 #include "lr_device.h"
 #include "lr_runtime.h"
 
+#ifndef GEMM_RING_A
+#define GEMM_RING_A 3
+#endif
+#ifndef GEMM_RING_B
+#define GEMM_RING_B 2
+#endif
+
 namespace lr {
 namespace {
 
@@ -136,12 +143,16 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_fast(GemmArgs p) 
   constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N;
   constexpr int FM = WM / 16, FN = WN / 16;
   constexpr int A_BYTES = BM * BK, B_BYTES = BN * BK;
-  constexpr int STAGE_BYTES = A_BYTES + B_BYTES;
   constexpr int A_LOADS = BM / 8 / NWAVES, B_LOADS = BN / 8 / NWAVES;  // 1 KB DMAs per wave per k-step
+  // A k-steps live in a ring of NA LDS slots, W k-steps in a ring of NB: an
+  // operand with 3 slots is fetched two k-steps ahead, with 2 one k-step.
+  constexpr int NA = GEMM_RING_A, NB = GEMM_RING_B;
   static_assert(NWAVES == 4 || NWAVES == 8, "4 or 8 waves");
   static_assert(A_LOADS * NWAVES * 8 == BM && B_LOADS * NWAVES * 8 == BN && A_LOADS >= 1 &&
                     B_LOADS >= 1 && FM >= 1 && FN >= 1, "tile shape");
-  __shared__ __attribute__((aligned(1024))) char smem[2 * STAGE_BYTES];
+  __shared__ __attribute__((aligned(1024))) char smem[NA * A_BYTES + NB * B_BYTES];
+  char* const a_ring = smem;
+  char* const b_ring = smem + NA * A_BYTES;
 
   int tm, tn;
   tile_coords(p, tm, tn);
@@ -161,35 +172,40 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_fast(GemmArgs p) 
   // DMA lane mapping: block kb covers rows 8kb..8kb+7; lane l writes slot
   // l % 8 of row 8kb + l / 8, which holds chunk (l % 8) ^ (l / 8).
   const int drow = lane >> 3;
-  auto dma_chunk = [&](int) { return ((lane & 7) ^ drow) * 16; };
+  const int dchunk = ((lane & 7) ^ drow) * 16;
   uint32_t a_off[A_LOADS], b_off[B_LOADS];
-  int a_chk[A_LOADS], b_chk[B_LOADS];
 #pragma unroll
-  for (int i = 0; i < A_LOADS; ++i) {
-    const int kb = wave * A_LOADS + i;
-    a_chk[i] = dma_chunk(kb);
-    a_off[i] = (uint32_t)((kb * 8 + drow) * K + a_chk[i]);
-  }
+  for (int i = 0; i < A_LOADS; ++i) a_off[i] = (uint32_t)(((wave * A_LOADS + i) * 8 + drow) * K + dchunk);
 #pragma unroll
-  for (int j = 0; j < B_LOADS; ++j) {
-    const int kb = wave * B_LOADS + j;
-    b_chk[j] = dma_chunk(kb);
-    b_off[j] = (uint32_t)((kb * 8 + drow) * K + b_chk[j]);
-  }
+  for (int j = 0; j < B_LOADS; ++j) b_off[j] = (uint32_t)(((wave * B_LOADS + j) * 8 + drow) * K + dchunk);
 
-  auto issue = [&](int kt, int stage) {
+  // k-steps past the end (the rings keep issuing so that the wait counts stay
+  // fixed) read as zero without touching memory.
+  auto dma_a = [&](int kt, int i) {
     const int64_t kbase = (int64_t)kt * BK;
-    const uint32_t kofs = (uint32_t)kbase;
-    char* sa = smem + stage * STAGE_BYTES;
-    char* sb = sa + A_BYTES;
+    dma16(ra, a_ring + (kt % NA) * A_BYTES + (wave * A_LOADS + i) * 1024,
+          kbase + dchunk < K ? a_off[i] + (uint32_t)kbase : 0x80000000u);
+  };
+  auto dma_b = [&](int kt, int j) {
+    const int64_t kbase = (int64_t)kt * BK;
+    dma16(rb, b_ring + (kt % NB) * B_BYTES + (wave * B_LOADS + j) * 1024,
+          kbase + dchunk < K ? b_off[j] + (uint32_t)kbase : 0x80000000u);
+  };
+  auto issue_a = [&](int kt) {
+    const int64_t kbase = (int64_t)kt * BK;
+    char* dst = a_ring + (kt % NA) * A_BYTES;
 #pragma unroll
     for (int i = 0; i < A_LOADS; ++i)
-      dma16(ra, sa + (wave * A_LOADS + i) * 1024,
-            kbase + a_chk[i] < K ? a_off[i] + kofs : 0x80000000u);
+      dma16(ra, dst + (wave * A_LOADS + i) * 1024,
+            kbase + dchunk < K ? a_off[i] + (uint32_t)kbase : 0x80000000u);
+  };
+  auto issue_b = [&](int kt) {
+    const int64_t kbase = (int64_t)kt * BK;
+    char* dst = b_ring + (kt % NB) * B_BYTES;
 #pragma unroll
     for (int j = 0; j < B_LOADS; ++j)
-      dma16(rb, sb + (wave * B_LOADS + j) * 1024,
-            kbase + b_chk[j] < K ? b_off[j] + kofs : 0x80000000u);
+      dma16(rb, dst + (wave * B_LOADS + j) * 1024,
+            kbase + dchunk < K ? b_off[j] + (uint32_t)kbase : 0x80000000u);
   };
 
   // Fragment read: 16-row fragment f spans blocks 2f, 2f+1.
@@ -208,33 +224,80 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_fast(GemmArgs p) 
 #pragma unroll
     for (int j = 0; j < FN; ++j) acc[i][j] = v4i{0, 0, 0, 0};
 
-  // Double buffer: wait for k-step kt's DMA, barrier (kt complete in LDS and
-  // every wave done with kt-1), start the DMA of kt+1 into the other buffer,
-  // then the MFMAs of kt with its fragments read from LDS. The two waves on
-  // each SIMD hide each other's LDS latency.
-  if (KT > 0) issue(0, 0);
+  // At the barrier of k-step kt the slots of k-step kt-1 are free; the
+  // shallower ring's next k-step is issued first, then the deeper ring's.
+  // Each wave's DMAs complete in issue order, so when k-step kt starts only
+  // the deeper ring's newest k-step may still be in flight.
+  static_assert((NA == 2 || NA == 3) && (NB == 2 || NB == 3), "ring depths");
+  constexpr int kLater = NA > NB ? A_LOADS : (NB > NA ? B_LOADS : 0);
+  constexpr int kWait = 0x70 | 0xf00 | (kLater & 0xf) | ((kLater >> 4) << 14);  // vmcnt(kLater)
+  if (NB <= NA) {
+    for (int s = 0; s < NB - 1; ++s) issue_b(s);
+    for (int s = 0; s < NA - 1; ++s) issue_a(s);
+  } else {
+    for (int s = 0; s < NA - 1; ++s) issue_a(s);
+    for (int s = 0; s < NB - 1; ++s) issue_b(s);
+  }
+  // One k-step: the first half's fragments are read, then its FM*FN MFMAs run
+  // with the second half's fragment reads and the shallower ring's DMAs
+  // interleaved, then the second half's MFMAs with the deeper ring's DMAs.
+  // Spreading the DMAs over the MFMAs keeps the vector-memory queue from
+  // stalling every wave at once right after the barrier; the scheduling
+  // barriers pin that order.
+  constexpr int NMF = FM * FN;
+  constexpr int NR1 = FM + FN;
+  constexpr bool B_FIRST = NB <= NA;
+  constexpr int L1 = B_FIRST ? B_LOADS : A_LOADS, L2 = B_FIRST ? A_LOADS : B_LOADS;
   for (int kt = 0; kt < KT; ++kt) {
-    __builtin_amdgcn_s_waitcnt(0x70 | 0xf00);  // vmcnt(0)
+    __builtin_amdgcn_s_waitcnt(kWait);
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
     __builtin_amdgcn_sched_barrier(0);
-    if (kt + 1 < KT) issue(kt + 1, (kt + 1) & 1);
-    const char* sa = smem + (kt & 1) * STAGE_BYTES;
-    const char* sb = sa + A_BYTES;
+    const char* sa = a_ring + (kt % NA) * A_BYTES;
+    const char* sb = b_ring + (kt % NB) * B_BYTES;
+    const int kt_b = kt + NB - 1, kt_a = kt + NA - 1;
+    v4i a0[FM], w0[FN], a1[FM], w1[FN];
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      v4i af[FM], wf[FN];
+    for (int j = 0; j < FN; ++j) w0[j] = frag(sb, wn * FN + j, 0);
 #pragma unroll
-      for (int j = 0; j < FN; ++j) wf[j] = frag(sb, wn * FN + j, h);
+    for (int i = 0; i < FM; ++i) a0[i] = frag(sa, wm * FM + i, 0);
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int i = 0; i < FM; ++i) af[i] = frag(sa, wm * FM + i, h);
+    for (int t = 0; t < NMF; ++t) {
+      const int i = t / FN, j = t % FN;
+      acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(w0[j], a0[i], acc[i][j], 0, 0, 0);
 #pragma unroll
-      for (int i = 0; i < FM; ++i)
+      for (int r = 0; r < NR1; ++r) {
+        if ((r * NMF) / NR1 == t) {
+          if (r < FN) w1[r] = frag(sb, wn * FN + r, 1);
+          else a1[r - FN] = frag(sa, wm * FM + (r - FN), 1);
+        }
+      }
 #pragma unroll
-        for (int j = 0; j < FN; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(wf[j], af[i], acc[i][j], 0, 0, 0);
+      for (int d = 0; d < L1; ++d) {
+        if ((d * NMF) / L1 == t) {
+          if (B_FIRST) dma_b(kt_b, d);
+          else dma_a(kt_a, d);
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int t = 0; t < NMF; ++t) {
+      const int i = t / FN, j = t % FN;
+      acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(w1[j], a1[i], acc[i][j], 0, 0, 0);
+#pragma unroll
+      for (int d = 0; d < L2; ++d) {
+        if ((d * NMF) / L2 == t) {
+          if (B_FIRST) dma_a(kt_a, d);
+          else dma_b(kt_b, d);
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
     }
   }
+  // The trailing zero-fill DMAs must land before the workgroup's LDS is freed.
+  __builtin_amdgcn_s_waitcnt(0x70 | 0xf00);  // vmcnt(0)
 
   // Epilogue. Lane l holds, for MFMA tile (i, j), row wm*WM + 16i + l%16 and
   // columns wn*WN + 16j + 4*(l/16) + 0..3.
