@@ -51,7 +51,8 @@ struct GemmArgs {
   int64_t table_rows, table_width, sequence;
   int gate_slot;
   int tiles_m, tiles_n, group_m;
-  int nvec;  // N % 4 == 0 and C/bias/col_scale/residual aligned for 4-wide access
+  int nvec;    // N % 4 == 0 and C/bias/col_scale/residual aligned for 4-wide access
+  int staged;  // nvec, N % 8 == 0 and 16-byte aligned C/residual/table rows: whole-line stores
 };
 
 enum { EPI_BF16 = LR_EPI_BF16, EPI_GELU = LR_EPI_GELU_TANH, EPI_GATED = LR_EPI_GATED_RESIDUAL,
@@ -113,6 +114,171 @@ __device__ __forceinline__ void tile_coords(const GemmArgs& p, int& tm, int& tn)
   const int within = lid - g * span;
   tm = first + within % gm;
   tn = within / gm;
+}
+
+// Epilogue of one wave's (16*FM) x (16*FN) sub-tile, stored from the MFMA
+// layout: lane l holds, for MFMA tile (i, j), row wm*WM + 16i + l%16 and
+// columns wn*WN + 16j + 4*(l/16) + 0..3 (8-byte stores; any N % 4 == 0).
+template <int FM, int FN, int WM, int WN, int EPI, bool BIAS>
+__device__ __forceinline__ void store_tile(const GemmArgs& p, const v4i (&acc)[FM][FN], int64_t m0,
+                                           int64_t n0, int wm, int wn, int lane) {
+  const int lr_ = lane & 15, lg = lane >> 4;
+  int64_t rows[FM];
+  float rsv[FM];
+  int64_t trow[FM];
+#pragma unroll
+  for (int i = 0; i < FM; ++i) {
+    rows[i] = m0 + wm * WM + 16 * i + lr_;
+    const bool ok = rows[i] < p.m;
+    rsv[i] = (EPI != EPI_RAW && ok) ? p.rs[rows[i]] : 0.0f;
+    trow[i] = (EPI == EPI_GATED && ok) ? table_row(p, rows[i]) : 0;
+  }
+#pragma unroll
+  for (int j = 0; j < FN; ++j) {
+    // Keep the column groups apart: hoisting every accumulator read to the
+    // top would need all 256 accumulators in VGPRs at once.
+    __builtin_amdgcn_sched_barrier(0);
+    const int64_t col = n0 + wn * WN + 16 * j + 4 * lg;
+    if (p.nvec) {
+      if (col >= p.n) continue;
+      if (EPI == EPI_RAW) {
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+          if (rows[i] < p.m)
+            *reinterpret_cast<v4i*>(static_cast<int32_t*>(p.c) + rows[i] * p.n + col) = acc[i][j];
+        continue;
+      }
+      const float4 cs = *reinterpret_cast<const float4*>(p.cs + col);
+      float b0 = 0.f, b1 = 0.f, b2 = 0.f, b3 = 0.f;
+      if (BIAS) {
+        const uint2 bb = *reinterpret_cast<const uint2*>(p.bias + col);
+        b0 = bf_lo(bb.x); b1 = bf_hi(bb.x); b2 = bf_lo(bb.y); b3 = bf_hi(bb.y);
+      }
+#pragma unroll
+      for (int i = 0; i < FM; ++i) {
+        if (rows[i] >= p.m) continue;
+        const int64_t o = rows[i] * p.n + col;
+        float v0 = dequant<BIAS>(acc[i][j][0], rsv[i], cs.x, b0);
+        float v1 = dequant<BIAS>(acc[i][j][1], rsv[i], cs.y, b1);
+        float v2 = dequant<BIAS>(acc[i][j][2], rsv[i], cs.z, b2);
+        float v3 = dequant<BIAS>(acc[i][j][3], rsv[i], cs.w, b3);
+        if (EPI == EPI_GATED) {
+          const uint2 xv = *reinterpret_cast<const uint2*>(p.resid + o);
+          const uint2 gv = *reinterpret_cast<const uint2*>(
+              p.table + trow[i] * p.table_width + (int64_t)p.gate_slot * p.n + col);
+          v0 = finish<EPI>(v0, bf_lo(gv.x), bf_lo(xv.x));
+          v1 = finish<EPI>(v1, bf_hi(gv.x), bf_hi(xv.x));
+          v2 = finish<EPI>(v2, bf_lo(gv.y), bf_lo(xv.y));
+          v3 = finish<EPI>(v3, bf_hi(gv.y), bf_hi(xv.y));
+        } else {
+          v0 = finish<EPI>(v0, 0.f, 0.f);
+          v1 = finish<EPI>(v1, 0.f, 0.f);
+          v2 = finish<EPI>(v2, 0.f, 0.f);
+          v3 = finish<EPI>(v3, 0.f, 0.f);
+        }
+        *reinterpret_cast<uint2*>(static_cast<uint16_t*>(p.c) + o) =
+            make_uint2(pack_bf2(v0, v1), pack_bf2(v2, v3));
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < FM; ++i) {
+        if (rows[i] >= p.m) continue;
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (col + e < p.n) store_scalar<EPI, BIAS>(p, rows[i], col + e, acc[i][j][e]);
+      }
+    }
+  }
+}
+
+__device__ __forceinline__ uint32_t word_of(const uint4& v, int i) {
+  return i == 0 ? v.x : (i == 1 ? v.y : (i == 2 ? v.z : v.w));
+}
+
+// Epilogue through the wave's LDS staging area (row pitch 2*WN + 16 bytes:
+// 16-byte aligned rows, and the MFMA-layout writes spread over the banks). Phase 1, in the MFMA layout:
+// bf16(((float)acc * rs) * cs + bias) into LDS; for GELU and the gated
+// residual this is exactly the bf16 value those epilogues start from. Phase 2,
+// row-major: each lane takes 8 consecutive columns of one row (16 bytes),
+// finishes the epilogue there (residual and gate read as 16-byte rows) and
+// stores them, so that every store instruction writes whole 128-byte lines.
+// Partial-line stores from the MFMA layout cost about twice the output bytes
+// in HBM writes. Needs N % 8 == 0 and 16-byte aligned C (and residual/table).
+template <int FM, int FN, int WM, int WN, int EPI, bool BIAS>
+__device__ __forceinline__ void store_tile_staged(const GemmArgs& p, const v4i (&acc)[FM][FN],
+                                                  char* stage, int64_t m0, int64_t n0, int wm,
+                                                  int wn, int lane) {
+  constexpr int PITCH = 2 * WN + 16;
+  const int lr_ = lane & 15, lg = lane >> 4;
+  float rsv[FM];
+#pragma unroll
+  for (int i = 0; i < FM; ++i) {
+    const int64_t row = m0 + wm * WM + 16 * i + lr_;
+    rsv[i] = row < p.m ? p.rs[row] : 0.0f;
+  }
+#pragma unroll
+  for (int j = 0; j < FN; ++j) {
+    __builtin_amdgcn_sched_barrier(0);
+    const int64_t col = n0 + wn * WN + 16 * j + 4 * lg;
+    float4 cs = make_float4(0.f, 0.f, 0.f, 0.f);
+    float b0 = 0.f, b1 = 0.f, b2 = 0.f, b3 = 0.f;
+    if (col < p.n) {
+      cs = *reinterpret_cast<const float4*>(p.cs + col);
+      if (BIAS) {
+        const uint2 bb = *reinterpret_cast<const uint2*>(p.bias + col);
+        b0 = bf_lo(bb.x); b1 = bf_hi(bb.x); b2 = bf_lo(bb.y); b3 = bf_hi(bb.y);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < FM; ++i) {
+      const float v0 = dequant<BIAS>(acc[i][j][0], rsv[i], cs.x, b0);
+      const float v1 = dequant<BIAS>(acc[i][j][1], rsv[i], cs.y, b1);
+      const float v2 = dequant<BIAS>(acc[i][j][2], rsv[i], cs.z, b2);
+      const float v3 = dequant<BIAS>(acc[i][j][3], rsv[i], cs.w, b3);
+      *reinterpret_cast<uint2*>(stage + (16 * i + lr_) * PITCH + (16 * j + 4 * lg) * 2) =
+          make_uint2(pack_bf2(v0, v1), pack_bf2(v2, v3));
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's staging writes are done
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+
+  constexpr int CPR = WN / 8;            // 16-byte chunks per row
+  constexpr int ITERS = WM * CPR / 64;   // rows of 16-byte chunks per lane
+  static_assert(WM * CPR % 64 == 0, "staging tile shape");
+  const bool seq_covers = p.sequence >= p.m;
+#pragma unroll 4
+  for (int s = 0; s < ITERS; ++s) {
+    const int q = s * 64 + lane;
+    const int r = q / CPR, ch = q % CPR;
+    const int64_t row = m0 + wm * WM + r;
+    const int64_t col = n0 + wn * WN + ch * 8;
+    uint4 v = *reinterpret_cast<const uint4*>(stage + r * PITCH + ch * 16);
+    if (row < p.m && col < p.n) {
+      const int64_t o = row * p.n + col;
+      if (EPI == EPI_GELU) {
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          const uint32_t u = word_of(v, w);
+          const uint32_t g = pack_bf2(fast_gelu_tanh(bf_lo(u)), fast_gelu_tanh(bf_hi(u)));
+          if (w == 0) v.x = g; else if (w == 1) v.y = g; else if (w == 2) v.z = g; else v.w = g;
+        }
+      } else if (EPI == EPI_GATED) {
+        const int64_t tr = clamp_index(p.indices[seq_covers ? row : row % p.sequence], p.table_rows);
+        const uint4 xv = *reinterpret_cast<const uint4*>(p.resid + o);
+        const uint4 gv = *reinterpret_cast<const uint4*>(
+            p.table + tr * p.table_width + (int64_t)p.gate_slot * p.n + col);
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          const uint32_t u = word_of(v, w), x = word_of(xv, w), g = word_of(gv, w);
+          const uint32_t y = pack_bf2(bf_lo(x) + round_bf(bf_lo(g) * bf_lo(u)),
+                                      bf_hi(x) + round_bf(bf_hi(g) * bf_hi(u)));
+          if (w == 0) v.x = y; else if (w == 1) v.y = y; else if (w == 2) v.z = y; else v.w = y;
+        }
+      }
+      *reinterpret_cast<uint4*>(static_cast<uint16_t*>(p.c) + o) = v;
+    }
+  }
 }
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
@@ -299,74 +465,15 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_fast(GemmArgs p) 
   // The trailing zero-fill DMAs must land before the workgroup's LDS is freed.
   __builtin_amdgcn_s_waitcnt(0x70 | 0xf00);  // vmcnt(0)
 
-  // Epilogue. Lane l holds, for MFMA tile (i, j), row wm*WM + 16i + l%16 and
-  // columns wn*WN + 16j + 4*(l/16) + 0..3.
-  const int lr_ = lane & 15, lg = lane >> 4;
-  int64_t rows[FM];
-  float rsv[FM];
-  int64_t trow[FM];
-#pragma unroll
-  for (int i = 0; i < FM; ++i) {
-    rows[i] = m0 + wm * WM + 16 * i + lr_;
-    const bool ok = rows[i] < p.m;
-    rsv[i] = (EPI != EPI_RAW && ok) ? p.rs[rows[i]] : 0.0f;
-    trow[i] = (EPI == EPI_GATED && ok) ? table_row(p, rows[i]) : 0;
-  }
-#pragma unroll
-  for (int j = 0; j < FN; ++j) {
-    // Keep the column groups apart: hoisting every accumulator read to the
-    // top would need all 256 accumulators in VGPRs at once.
-    __builtin_amdgcn_sched_barrier(0);
-    const int64_t col = n0 + wn * WN + 16 * j + 4 * lg;
-    if (p.nvec) {
-      if (col >= p.n) continue;
-      if (EPI == EPI_RAW) {
-#pragma unroll
-        for (int i = 0; i < FM; ++i)
-          if (rows[i] < p.m)
-            *reinterpret_cast<v4i*>(static_cast<int32_t*>(p.c) + rows[i] * p.n + col) = acc[i][j];
-        continue;
-      }
-      const float4 cs = *reinterpret_cast<const float4*>(p.cs + col);
-      float b0 = 0.f, b1 = 0.f, b2 = 0.f, b3 = 0.f;
-      if (BIAS) {
-        const uint2 bb = *reinterpret_cast<const uint2*>(p.bias + col);
-        b0 = bf_lo(bb.x); b1 = bf_hi(bb.x); b2 = bf_lo(bb.y); b3 = bf_hi(bb.y);
-      }
-#pragma unroll
-      for (int i = 0; i < FM; ++i) {
-        if (rows[i] >= p.m) continue;
-        const int64_t o = rows[i] * p.n + col;
-        float v0 = dequant<BIAS>(acc[i][j][0], rsv[i], cs.x, b0);
-        float v1 = dequant<BIAS>(acc[i][j][1], rsv[i], cs.y, b1);
-        float v2 = dequant<BIAS>(acc[i][j][2], rsv[i], cs.z, b2);
-        float v3 = dequant<BIAS>(acc[i][j][3], rsv[i], cs.w, b3);
-        if (EPI == EPI_GATED) {
-          const uint2 xv = *reinterpret_cast<const uint2*>(p.resid + o);
-          const uint2 gv = *reinterpret_cast<const uint2*>(
-              p.table + trow[i] * p.table_width + (int64_t)p.gate_slot * p.n + col);
-          v0 = finish<EPI>(v0, bf_lo(gv.x), bf_lo(xv.x));
-          v1 = finish<EPI>(v1, bf_hi(gv.x), bf_hi(xv.x));
-          v2 = finish<EPI>(v2, bf_lo(gv.y), bf_lo(xv.y));
-          v3 = finish<EPI>(v3, bf_hi(gv.y), bf_hi(xv.y));
-        } else {
-          v0 = finish<EPI>(v0, 0.f, 0.f);
-          v1 = finish<EPI>(v1, 0.f, 0.f);
-          v2 = finish<EPI>(v2, 0.f, 0.f);
-          v3 = finish<EPI>(v3, 0.f, 0.f);
-        }
-        *reinterpret_cast<uint2*>(static_cast<uint16_t*>(p.c) + o) =
-            make_uint2(pack_bf2(v0, v1), pack_bf2(v2, v3));
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < FM; ++i) {
-        if (rows[i] >= p.m) continue;
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-          if (col + e < p.n) store_scalar<EPI, BIAS>(p, rows[i], col + e, acc[i][j][e]);
-      }
-    }
+  if (EPI != EPI_RAW && p.staged) {
+    // Whole-line stores through LDS: every wave must be done reading the
+    // operand stages before they are overwritten.
+    static_assert(NWAVES * WM * (2 * WN + 16) <= (int)sizeof(smem), "staging fits in LDS");
+    __syncthreads();
+    store_tile_staged<FM, FN, WM, WN, EPI, BIAS>(p, acc, smem + wave * WM * (2 * WN + 16), m0, n0,
+                                                 wm, wn, lane);
+  } else {
+    store_tile<FM, FN, WM, WN, EPI, BIAS>(p, acc, m0, n0, wm, wn, lane);
   }
 }
 
@@ -524,6 +631,10 @@ extern "C" int lr_int8_gemm(const int8_t* a, const int8_t* b, int64_t b_stride_k
            (bias == nullptr || aligned(bias, 8)) &&
            (epilogue != LR_EPI_GATED_RESIDUAL ||
             (aligned(residual, 8) && aligned(table, 8) && table_width % 4 == 0));
+
+  p.staged = p.nvec && n % 8 == 0 && aligned(c, 16) &&
+             (epilogue != LR_EPI_GATED_RESIDUAL ||
+              (aligned(residual, 16) && aligned(table, 16) && table_width % 8 == 0));
 
   // Fast path: W stored [N,K] row-major with 16-byte aligned rows; buffer
   // descriptors need per-block ranges (256 rows * K) below 2^31 bytes.
