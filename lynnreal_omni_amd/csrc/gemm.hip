@@ -316,7 +316,11 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_fast(GemmArgs p) 
   static_assert(NWAVES == 4 || NWAVES == 8, "4 or 8 waves");
   static_assert(A_LOADS * NWAVES * 8 == BM && B_LOADS * NWAVES * 8 == BN && A_LOADS >= 1 &&
                     B_LOADS >= 1 && FM >= 1 && FN >= 1, "tile shape");
-  __shared__ __attribute__((aligned(1024))) char smem[NA * A_BYTES + NB * B_BYTES];
+  // The operand rings, reused after the main loop as the epilogue's staging tiles.
+  constexpr int RING_BYTES = NA * A_BYTES + NB * B_BYTES;
+  constexpr int STAGING_BYTES = NWAVES * WM * (2 * WN + 16);
+  __shared__ __attribute__((aligned(1024)))
+  char smem[RING_BYTES > STAGING_BYTES ? RING_BYTES : STAGING_BYTES];
   char* const a_ring = smem;
   char* const b_ring = smem + NA * A_BYTES;
 
