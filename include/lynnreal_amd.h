@@ -168,6 +168,27 @@ int lr_swiglu_quant(const void* p, int8_t* q, float* scales, int64_t rows, int64
  * comfyui/custom_nodes/ComfyUI-LynnReal/tools/verify_sampling_safety.py:59. */
 int lr_gelu_tanh(const void* x, void* out, int64_t count, void* stream);
 
+/* Per-head RMSNorm of Q and K fused with rotary embedding. Replaces the
+ * launches at model/fusion.py:35-52 of model/kernels.py:187-257
+ * (_qk_norm_full_rope_paired_kernel, rotary_dim == head_dim) and :345-402
+ * (_qk_norm_rope_kernel, rotary_dim < head_dim). Per (batch, token, head)
+ * row of q (k likewise with k_weight):
+ *   rstd = 1 / sqrt(sumsq(row) / head_dim + eps), n = bf16((row * rstd) * w)
+ *   d <  rotary_dim/2: out = bf16(bf16(n[d]*c[d]) - bf16(n[d + rotary_dim/2]*s[d]))
+ *   d <  rotary_dim:   out = bf16(bf16(n[d]*c[d]) + bf16(n[d - rotary_dim/2]*s[d]))
+ *   d >= rotary_dim:   out = n[d]
+ * with c, s = bf16(cos/sin[token, d]) from fp32 [sequence, rotary_dim]. The
+ * sum of squares is in 8-element chunks (fma, element order), chunk j in slot
+ * j, slots combined by s[i] += s[i + h], h = head_dim/16 .. 1. q/k element
+ * (b, t, h, d) is at b*sequence*token_stride + t*token_stride + h*head_stride
+ * + d (bf16 elements); q_out/k_out are contiguous [batch, sequence, heads,
+ * head_dim]. head_dim in {32, 64, 128}; rotary_dim 0 or 16 * 2^n. */
+int lr_qk_norm_rope(const void* q, const void* k, const void* q_weight, const void* k_weight,
+                    const float* cos, const float* sin, void* q_out, void* k_out, int64_t batch,
+                    int64_t sequence, int64_t heads, int64_t q_token_stride, int64_t q_head_stride,
+                    int64_t k_token_stride, int64_t k_head_stride, int64_t head_dim,
+                    int64_t rotary_dim, float eps, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -48,6 +48,8 @@ SIGNATURES = {
     "lr_swiglu": [_P, _P, _I64, _I64, _P],
     "lr_swiglu_quant": [_P, _P, _P, _I64, _I64, _P],
     "lr_gelu_tanh": [_P, _P, _I64, _P],
+    "lr_qk_norm_rope": [_P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64,
+                        _I64, _I64, _F32, _P],
     "lr_device_supported": [_I32],
     "lr_abi_version": [],
     "lr_gemm_set_group_m": [_I32],

@@ -1,0 +1,221 @@
+// qknorm.hip - fused per-head RMSNorm of Q and K with rotary embedding.
+//
+// Restates model/kernels.py:187-257 (_qk_norm_full_rope_paired_kernel,
+// rotary_dim == head_dim) and :345-402 (_qk_norm_rope_kernel, rotary_dim <
+// head_dim), launched from model/fusion.py:35-52 between the QKV projection
+// and attention. Per (batch, token, head) row of Q, and of K with its own
+// weight:
+//   rstd = 1 / sqrt(sumsq(row) / head_dim + eps)
+//   n[d] = bf16((row[d] * rstd) * weight[d])
+//   d < rotary_dim, half = rotary_dim / 2, c/s = bf16(cos/sin[token, d]):
+//     d <  half: out = bf16(bf16(n[d] * c) - bf16(n[d + half] * s))
+//     d >= half: out = bf16(bf16(n[d] * c) + bf16(n[d - half] * s))
+//   d >= rotary_dim: out = n[d]
+//
+// One row takes L = head_dim / 8 lanes (16 bytes of Q and of K each), so a
+// wave holds 64 / L rows. The sum of squares follows the reference's ordered
+// reduction (model/kernels.py:333-344, _sum128): 32-element chunks, each
+// reduced by the tree s[i] += s[i + h], h = 16 .. 1, then the chunk sums by
+// the same tree ((s0 + s2) + (s1 + s3) for four chunks). Lane j = 4c + a
+// holds elements 32c + 8a + e, e < 8, so h = 16 and 8 pair lanes a ^ 2 and
+// a ^ 1 element by element (DPP), h = 4, 2, 1 stay inside the lane, and the
+// chunk tree pairs lanes j ^ 8 and j ^ 4. The rotary partner of chunk j is
+// chunk j ^ (rotary_dim / 16), fetched from that lane with DPP, so Q and K
+// are each read once.
+#include "lr_device.h"
+#include "lr_runtime.h"
+
+namespace lr {
+namespace {
+
+struct QkArgs {
+  const uint16_t* q;
+  const uint16_t* k;
+  const uint16_t* qw;
+  const uint16_t* kw;
+  const float* cos;
+  const float* sin;
+  uint16_t* qo;
+  uint16_t* ko;
+  int64_t rows, sequence, heads, q_ts, q_hs, k_ts, k_hs, head_dim, rotary_dim;
+  float eps;
+};
+
+template <int O>
+__device__ __forceinline__ uint32_t xor_word(uint32_t w) {
+  return __float_as_uint(xor_partner<O>(__uint_as_float(w)));
+}
+
+template <int O>
+__device__ __forceinline__ uint4 xor_chunk(const uint4& v) {
+  return make_uint4(xor_word<O>(v.x), xor_word<O>(v.y), xor_word<O>(v.z), xor_word<O>(v.w));
+}
+
+// n = bf16((x * rstd) * w) for the 8 elements of a chunk, packed.
+__device__ __forceinline__ uint4 normalize8(const uint4& x, const uint4& w, float rstd) {
+  float xf[8], wf[8];
+  unpack8(x, xf);
+  unpack8(w, wf);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) xf[e] = (xf[e] * rstd) * wf[e];
+  return pack8(xf);
+}
+
+__device__ __forceinline__ float rsqrt_row(float eps, int64_t head_dim, float s) {
+  const float ms = s / (float)head_dim + eps;
+  return 1.0f / __builtin_sqrtf(ms);
+}
+
+// Sum of squares of the row whose 8-element slice this lane holds, in the
+// order described at the top of the file. Squares of bf16 values are exact.
+template <int L>
+__device__ __forceinline__ float sumsq8(const uint4& x) {
+  float v[8];
+  unpack8(x, v);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) v[e] = v[e] * v[e];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) v[e] = v[e] + xor_partner<2>(v[e]);   // h = 16
+#pragma unroll
+  for (int e = 0; e < 8; ++e) v[e] = v[e] + xor_partner<1>(v[e]);   // h = 8
+#pragma unroll
+  for (int e = 0; e < 4; ++e) v[e] = v[e] + v[e + 4];                // h = 4
+  v[0] = v[0] + v[2];
+  v[1] = v[1] + v[3];                                                // h = 2
+  float s = v[0] + v[1];                                             // h = 1
+  if (L >= 16) s = s + xor_partner<8>(s);                            // chunk c + 2
+  if (L >= 8) s = s + xor_partner<4>(s);                             // chunk c + 1
+  return s;
+}
+
+// out = bf16(bf16(n * c) -/+ bf16(np * s)) over a chunk; `left` picks '-'.
+__device__ __forceinline__ uint4 rotate8(const uint4& n, const uint4& np, const float c[8],
+                                         const float s[8], bool left) {
+  float nf[8], pf[8];
+  unpack8(n, nf);
+  unpack8(np, pf);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float a = round_bf(nf[e] * c[e]);
+    const float b = round_bf(pf[e] * s[e]);
+    nf[e] = left ? a - b : a + b;
+  }
+  return pack8(nf);
+}
+
+// L lanes per row (head_dim = 8L); D = rotary_dim / 16 (0: no rotary).
+template <int L, int D>
+__global__ __launch_bounds__(256) void qk_norm_rope(QkArgs p) {
+  constexpr int RPW = 64 / L;  // rows per wave
+  const int lane = threadIdx.x & 63;
+  const int j = lane % L;
+  const int64_t row = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * RPW + lane / L;
+  const bool valid = row < p.rows;
+  const int64_t h = valid ? row % p.heads : 0;
+  const int64_t t = valid ? (row / p.heads) % p.sequence : 0;
+  const int64_t b = valid ? row / (p.heads * p.sequence) : 0;
+
+  uint4 qx = make_uint4(0, 0, 0, 0), kx = qx;
+  if (valid) {
+    qx = *reinterpret_cast<const uint4*>(p.q + b * p.sequence * p.q_ts + t * p.q_ts + h * p.q_hs + 8 * j);
+    kx = *reinterpret_cast<const uint4*>(p.k + b * p.sequence * p.k_ts + t * p.k_ts + h * p.k_hs + 8 * j);
+  }
+  // Every lane takes part in the cross-lane steps; rows past the end hold zeros.
+  const float q_rstd = rsqrt_row(p.eps, p.head_dim, sumsq8<L>(qx));
+  const float k_rstd = rsqrt_row(p.eps, p.head_dim, sumsq8<L>(kx));
+  const uint4 qw = *reinterpret_cast<const uint4*>(p.qw + 8 * j);
+  const uint4 kw = *reinterpret_cast<const uint4*>(p.kw + 8 * j);
+  uint4 qn = normalize8(qx, qw, q_rstd);
+  uint4 kn = normalize8(kx, kw, k_rstd);
+  if (D > 0) {
+    const uint4 qp = xor_chunk<D>(qn);
+    const uint4 kp = xor_chunk<D>(kn);
+    if (j < 2 * D && valid) {
+      float c[8], s[8];
+      const float4* cr = reinterpret_cast<const float4*>(p.cos + t * p.rotary_dim + 8 * j);
+      const float4* sr = reinterpret_cast<const float4*>(p.sin + t * p.rotary_dim + 8 * j);
+      const float4 c0 = cr[0], c1 = cr[1], s0 = sr[0], s1 = sr[1];
+      c[0] = c0.x; c[1] = c0.y; c[2] = c0.z; c[3] = c0.w; c[4] = c1.x; c[5] = c1.y; c[6] = c1.z; c[7] = c1.w;
+      s[0] = s0.x; s[1] = s0.y; s[2] = s0.z; s[3] = s0.w; s[4] = s1.x; s[5] = s1.y; s[6] = s1.z; s[7] = s1.w;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) c[e] = round_bf(c[e]), s[e] = round_bf(s[e]);
+      const bool left = (j & D) == 0;
+      qn = rotate8(qn, qp, c, s, left);
+      kn = rotate8(kn, kp, c, s, left);
+    }
+  }
+  if (valid) {
+    *reinterpret_cast<uint4*>(p.qo + row * p.head_dim + 8 * j) = qn;
+    *reinterpret_cast<uint4*>(p.ko + row * p.head_dim + 8 * j) = kn;
+  }
+}
+
+template <int L, int D>
+void launch(const QkArgs& p, hipStream_t st) {
+  const int64_t rows_per_block = 4 * (64 / L);
+  const int64_t blocks = (p.rows + rows_per_block - 1) / rows_per_block;
+  hipLaunchKernelGGL((qk_norm_rope<L, D>), dim3((unsigned)blocks), dim3(256), 0, st, p);
+}
+
+template <int L>
+int launch_rot(const QkArgs& p, hipStream_t st) {
+  // rotary_dim <= head_dim = 8L keeps the pair distance D = rotary_dim / 16 below L.
+  switch (p.rotary_dim / 16) {
+    case 0: launch<L, 0>(p, st); break;
+    case 1: launch<L, 1>(p, st); break;
+    case 2: if constexpr (L >= 4) launch<L, 2>(p, st); break;
+    case 4: if constexpr (L >= 8) launch<L, 4>(p, st); break;
+    case 8: if constexpr (L >= 16) launch<L, 8>(p, st); break;
+    default: return fail(LR_EUNSUPPORTED, "qk_norm_rope: rotary_dim %lld not supported",
+                         (long long)p.rotary_dim);
+  }
+  return check_launch("qk_norm_rope");
+}
+
+}  // namespace
+}  // namespace lr
+
+using namespace lr;
+
+extern "C" int lr_qk_norm_rope(const void* q, const void* k, const void* q_weight,
+                               const void* k_weight, const float* cos, const float* sin,
+                               void* q_out, void* k_out, int64_t batch, int64_t sequence,
+                               int64_t heads, int64_t q_token_stride, int64_t q_head_stride,
+                               int64_t k_token_stride, int64_t k_head_stride, int64_t head_dim,
+                               int64_t rotary_dim, float eps, void* stream) {
+  LR_REQUIRE(batch >= 0 && sequence >= 0 && heads >= 0, "qk_norm_rope: negative shape");
+  const int64_t rows = batch * sequence * heads;
+  if (rows == 0) return LR_OK;
+  LR_REQUIRE(q && k && q_weight && k_weight && q_out && k_out, "qk_norm_rope: null pointer");
+  LR_REQUIRE(rotary_dim >= 0 && rotary_dim <= head_dim && rotary_dim % 2 == 0,
+             "qk_norm_rope: rotary dimensions must be even and fit the attention head");
+  LR_REQUIRE(rotary_dim == 0 || (cos && sin), "qk_norm_rope: null cos/sin");
+  if (!(head_dim == 32 || head_dim == 64 || head_dim == 128))
+    return fail(LR_EUNSUPPORTED, "qk_norm_rope: head_dim %lld not supported (32, 64, 128)",
+                (long long)head_dim);
+  const int64_t r16 = rotary_dim / 16;
+  if (rotary_dim % 16 != 0 || (r16 & (r16 - 1)) != 0)
+    return fail(LR_EUNSUPPORTED, "qk_norm_rope: rotary_dim %lld not supported (0 or 16 * 2^n)",
+                (long long)rotary_dim);
+  const bool aligned_ok = aligned(q, 16) && aligned(k, 16) && aligned(q_weight, 16) &&
+                          aligned(k_weight, 16) && aligned(q_out, 16) && aligned(k_out, 16) &&
+                          q_token_stride % 8 == 0 && q_head_stride % 8 == 0 &&
+                          k_token_stride % 8 == 0 && k_head_stride % 8 == 0 &&
+                          (rotary_dim == 0 || (aligned(cos, 16) && aligned(sin, 16)));
+  if (!aligned_ok)
+    return fail(LR_EUNSUPPORTED, "qk_norm_rope: rows must be 16-byte aligned");
+  LR_REQUIRE(rows / (4 * (64 / (head_dim / 8))) < 0x7fffffffLL, "qk_norm_rope: too many rows");
+  QkArgs p{};
+  p.q = (const uint16_t*)q; p.k = (const uint16_t*)k;
+  p.qw = (const uint16_t*)q_weight; p.kw = (const uint16_t*)k_weight;
+  p.cos = cos; p.sin = sin; p.qo = (uint16_t*)q_out; p.ko = (uint16_t*)k_out;
+  p.rows = rows; p.sequence = sequence; p.heads = heads;
+  p.q_ts = q_token_stride; p.q_hs = q_head_stride; p.k_ts = k_token_stride; p.k_hs = k_head_stride;
+  p.head_dim = head_dim; p.rotary_dim = rotary_dim; p.eps = eps;
+  hipStream_t st = as_stream(stream);
+  switch (head_dim) {
+    case 32: return launch_rot<4>(p, st);
+    case 64: return launch_rot<8>(p, st);
+    default: return launch_rot<16>(p, st);
+  }
+}

@@ -17,6 +17,8 @@ Arithmetic (all fp32 with the reference's bf16 rounding points):
   _gated_residual      bf16(x + bf16(gate*u))                 kernels.py:131-153
   _swiglu(_quant)      bf16(v * bf16(g*sigmoid(g))) (-> INT8)  kernels.py:156-185
   gelu_tanh            bf16(gelu_tanh(x))  (new: the BASELINE FFN activation)
+  qk_norm_rope         per-head RMSNorm of Q/K -> bf16, RoPE with bf16 products
+                                                              kernels.py:187-257,345-402
 
 The RMSNorm sum of squares uses one fixed reduction order (documented in
 include/lynnreal_amd.h) and an IEEE 1/sqrt, so the bf16 outputs reproduce a
@@ -196,3 +198,53 @@ def gelu_tanh(value):
     _lib.call("lr_gelu_tanh", value.data_ptr(), output.data_ptr(), value.numel(),
               _lib.stream(value))
     return output
+
+
+def qk_norm_rope(query, key, query_weight, key_weight, rotary_emb, eps):
+    """Per-head RMSNorm of Q and K fused with RoPE (model/fusion.py:35-52).
+
+    query, key: bf16 [batch, sequence, heads, head_dim] with contiguous heads
+    (views into a fused QKV tensor are fine); query_weight, key_weight: bf16
+    [head_dim] (attn.norm_q/norm_k weights); rotary_emb: (cos, sin), each
+    [sequence, rotary_dim] (rounded to bf16 in the kernel, as the reference
+    does). Returns new contiguous (q_out, k_out) like query. Both of the
+    reference's kernels (full-width paired RoPE and partial RoPE) are this one
+    launch; rotary_dim == 0 gives the bare RMSNorm.
+    """
+    cos, sin = rotary_emb
+    rotary_dim = cos.shape[-1]
+    if query.dim() != 4 or key.shape != query.shape:
+        raise ValueError("query and key must be [batch, sequence, heads, head_dim] of one shape")
+    head_dim = query.shape[-1]
+    if rotary_dim > head_dim or rotary_dim % 2:
+        raise ValueError("rotary dimensions must be even and fit the attention head")
+    for name, t in (("query", query), ("key", key)):
+        if t.dtype != torch.bfloat16:
+            raise ValueError(f"{name} must be bfloat16, got {t.dtype}")
+    _lib.check_device(query)
+
+    def rows(t):
+        # Element (b, t, h, d) must sit at b*S*token_stride + t*token_stride + h*head_stride + d.
+        if t.stride(3) != 1 or t.stride(0) != t.shape[1] * t.stride(1):
+            t = t.contiguous()
+        return t
+
+    query, key = rows(query), rows(key)
+    query_weight = _bf16(query_weight.reshape(-1), "query_weight")
+    key_weight = _bf16(key_weight.reshape(-1), "key_weight")
+    if cos.shape != sin.shape:
+        raise ValueError("cos and sin tables must have one shape")
+    batch, sequence, heads, _ = query.shape
+    if rotary_dim:
+        cos = cos.to(torch.float32).reshape(-1, rotary_dim).contiguous()
+        sin = sin.to(torch.float32).reshape(-1, rotary_dim).contiguous()
+        if cos.shape[0] < sequence:
+            raise ValueError(f"rotary tables have {cos.shape[0]} positions for {sequence} tokens")
+    q_out = torch.empty(query.shape, device=query.device, dtype=query.dtype)
+    k_out = torch.empty_like(q_out)
+    _lib.call("lr_qk_norm_rope", query.data_ptr(), key.data_ptr(), query_weight.data_ptr(),
+              key_weight.data_ptr(), cos.data_ptr() if rotary_dim else None,
+              sin.data_ptr() if rotary_dim else None, q_out.data_ptr(),
+              k_out.data_ptr(), batch, sequence, heads, query.stride(1), query.stride(2),
+              key.stride(1), key.stride(2), head_dim, rotary_dim, float(eps), _lib.stream(query))
+    return q_out, k_out

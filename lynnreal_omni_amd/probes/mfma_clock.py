@@ -18,6 +18,7 @@ def main() -> int:
     if not exe.exists() or exe.stat().st_mtime < src.stat().st_mtime:
         hipcc = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
         subprocess.run([hipcc, "--offload-arch=gfx950", "-O3", "-mllvm", "-amdgpu-mfma-vgpr-form",
+                        "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
                         str(src), "-o", str(exe)], check=True)
     return subprocess.run([str(exe)]).returncode
 

@@ -285,6 +285,84 @@ float lro_canonical_sumsq(const uint16_t* x, int64_t hidden) {
   return s;
 }
 
+/* ---------------------------------------------- QK RMSNorm + RoPE --- */
+/* model/kernels.py:187-257 (_qk_norm_full_rope_paired_kernel, rotary_dim ==
+ * head_dim) and :345-402 (_qk_norm_rope_kernel, rotary_dim < head_dim), as
+ * called from model/fusion.py:35-52. Per (batch, token, head) row of q (and
+ * of k, with its own weight):
+ *   rstd = 1 / sqrt(sumsq(row) / head_dim + eps)
+ *   n[d] = bf16((row[d] * rstd) * weight[d])
+ *   for d < rotary_dim, half = rotary_dim / 2, c/s = bf16(cos/sin[token, d]):
+ *     d <  half: out = bf16(bf16(n[d] * c) - bf16(n[d + half] * s))
+ *     d >= half: out = bf16(bf16(n[d] * c) + bf16(n[d - half] * s))
+ *   for d >= rotary_dim: out = n[d].
+ * The sum of squares follows the reference's ordered reduction for 128-wide
+ * heads (model/kernels.py:333-344, _sum128), which script/precompile.py:12-33
+ * checks equal to its four-warp tl.sum: the row is cut into 32-element
+ * chunks; each chunk's squares are reduced by the tree s[i] += s[i + h],
+ * h = 16, ..., 1 (a warp butterfly), and the chunk sums by the same tree
+ * (four chunks: (s0 + s2) + (s1 + s3)). 64- and 32-wide heads use the same
+ * rule with two chunks and one. Squares of bf16 values are exact in fp32, so
+ * fused or separate multiply-adds give the same sums. The reference's
+ * approximate tl.rsqrt is not reproducible here; rstd = 1 / sqrt(.) instead,
+ * and against the reference outputs agree to the bound that a 1-ulp change of
+ * the normalized value propagates to. q/k element (b, t, h, d) is at
+ * b*sequence*token_stride + t*token_stride + h*head_stride + d; outputs are
+ * contiguous [batch, sequence, heads, head_dim]. */
+static float qk_sumsq(const uint16_t* row, int64_t head_dim) {
+  float chunk[16];
+  const int64_t chunks = head_dim / 32;
+  for (int64_t c = 0; c < chunks; ++c) {
+    float s[32];
+    for (int i = 0; i < 32; ++i) s[i] = bf2f(row[32 * c + i]) * bf2f(row[32 * c + i]);
+    for (int h = 16; h >= 1; h /= 2)
+      for (int i = 0; i < h; ++i) s[i] = s[i] + s[i + h];
+    chunk[c] = s[0];
+  }
+  for (int64_t h = chunks / 2; h >= 1; h /= 2)
+    for (int64_t i = 0; i < h; ++i) chunk[i] = chunk[i] + chunk[i + h];
+  return chunk[0];
+}
+
+static void qk_row(const uint16_t* x, const uint16_t* w, const float* cos_row, const float* sin_row,
+                   int64_t head_dim, int64_t rotary_dim, float eps, uint16_t* out) {
+  float n[512];
+  const float ms = qk_sumsq(x, head_dim) / (float)head_dim + eps;
+  const float rstd = 1.0f / sqrtf(ms);
+  for (int64_t d = 0; d < head_dim; ++d) n[d] = rbf((bf2f(x[d]) * rstd) * bf2f(w[d]));
+  const int64_t half = rotary_dim / 2;
+  for (int64_t d = 0; d < head_dim; ++d) {
+    if (d < rotary_dim) {
+      const float c = rbf(cos_row[d]), s = rbf(sin_row[d]);
+      const float a = rbf(n[d] * c);
+      const float b = d < half ? rbf(n[d + half] * s) : rbf(n[d - half] * s);
+      out[d] = f2bf(d < half ? a - b : a + b);
+    } else {
+      out[d] = f2bf(n[d]);
+    }
+  }
+}
+
+float lro_qk_sumsq(const uint16_t* row, int64_t head_dim) { return qk_sumsq(row, head_dim); }
+
+void lro_qk_norm_rope(const uint16_t* q, const uint16_t* k, const uint16_t* qw, const uint16_t* kw,
+                      const float* cosv, const float* sinv, uint16_t* q_out, uint16_t* k_out,
+                      int64_t batch, int64_t sequence, int64_t heads, int64_t q_token_stride,
+                      int64_t q_head_stride, int64_t k_token_stride, int64_t k_head_stride,
+                      int64_t head_dim, int64_t rotary_dim, float eps) {
+  const int64_t rows = batch * sequence * heads;
+#pragma omp parallel for schedule(static)
+  for (int64_t r = 0; r < rows; ++r) {
+    const int64_t h = r % heads, t = (r / heads) % sequence, b = r / (heads * sequence);
+    const uint16_t* qr = q + b * sequence * q_token_stride + t * q_token_stride + h * q_head_stride;
+    const uint16_t* kr = k + b * sequence * k_token_stride + t * k_token_stride + h * k_head_stride;
+    qk_row(qr, qw, cosv + t * rotary_dim, sinv + t * rotary_dim, head_dim, rotary_dim, eps,
+           q_out + r * head_dim);
+    qk_row(kr, kw, cosv + t * rotary_dim, sinv + t * rotary_dim, head_dim, rotary_dim, eps,
+           k_out + r * head_dim);
+  }
+}
+
 int lro_num_threads(void) {
 #ifdef _OPENMP
   return omp_get_max_threads();

@@ -33,6 +33,8 @@ _SIGS = {
     "lro_residual_rms_quant": ([_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _F32, _P, _P,
                                 _P], None),
     "lro_canonical_sumsq": ([_P, _I64], ctypes.c_float),
+    "lro_qk_norm_rope": ([_P] * 8 + [_I64] * 9 + [_F32], None),
+    "lro_qk_sumsq": ([_P, _I64], ctypes.c_float),
     "lro_num_threads": ([], ctypes.c_int),
 }
 
@@ -200,6 +202,33 @@ def residual_rms_quant(x, u, w, table, indices, eps, sequence=None):
     load().lro_residual_rms_quant(_p(x), _p(u), _p(w), _p(table), _p(idx), rows, seq, hidden,
                                   trows, width, float(eps), _p(resid), _p(q), _p(s))
     return resid, q, s
+
+
+def qk_norm_rope(q, k, q_weight, k_weight, cos, sin, eps):
+    """model/kernels.py:187-257 and :345-402, sum of squares in the order of
+    the reference's ordered reduction (kernels.py:333-344).
+
+    q, k: bf16 bit patterns [batch, sequence, heads, head_dim] (copied
+    contiguous); weights [head_dim]; cos, sin: fp32 [sequence, rotary_dim].
+    Returns (q_out, k_out) contiguous like q.
+    """
+    q = _c(q, np.uint16)
+    k = _c(k, np.uint16)
+    batch, seq, heads, dim = q.shape
+    cos = _c(cos, np.float32)
+    sin = _c(sin, np.float32)
+    rot = cos.shape[-1]
+    qo = np.empty_like(q)
+    ko = np.empty_like(k)
+    load().lro_qk_norm_rope(_p(q), _p(k), _p(_c(q_weight, np.uint16)), _p(_c(k_weight, np.uint16)),
+                            _p(cos), _p(sin), _p(qo), _p(ko), batch, seq, heads, heads * dim, dim,
+                            heads * dim, dim, dim, rot, float(eps))
+    return qo, ko
+
+
+def qk_sumsq(row):
+    row = _c(row, np.uint16)
+    return float(load().lro_qk_sumsq(_p(row), row.size))
 
 
 def canonical_sumsq(row):

@@ -62,3 +62,31 @@ def assert_bf16_close(actual_u16, expected_u16, *, max_ulp=1, frac_exact=0.999, 
     denom = np.linalg.norm(af) * np.linalg.norm(ef)
     if denom > 0:
         assert float(af @ ef) / denom >= cos
+
+
+def assert_rope_close(actual_u16, expected_u16, rotary_dim, frac_exact=0.99):
+    """Tolerance for QK-RMSNorm + RoPE outputs whose sum of squares is
+    reduced in a different order from the expected values.
+
+    The normalized value n = bf16(x * rstd * w) may differ by one bf16 ulp.
+    Unrotated dimensions are exactly n, so they stay within 1 ulp. A rotated
+    output is bf16(a -/+ b) with a = bf16(n * c), b = bf16(n' * s), |c|, |s|
+    <= 1: a 1-ulp change of n moves a (and b) by at most 2 ulps of their own
+    magnitude, 2 * 2^-7 * |a|, and the output rounding adds 2^-8 * |out|. With
+    |a|, |b| <= max |n| over the row, and rotation keeping each (n, n') pair's
+    length, max |n| is within rounding of the largest output of the row:
+      |out - expected| <= 2^-5 * max_row |expected| * 1.02 + 2^-7 * |expected|.
+    Cancellation (a ~ b) makes a ulp count of the output meaningless there,
+    hence the absolute bound. At least `frac_exact` must be identical."""
+    a = np.asarray(actual_u16, np.uint16)
+    e = np.asarray(expected_u16, np.uint16)
+    assert a.shape == e.shape
+    ulp = bf16.ulp_distance(a, e)
+    assert float((ulp == 0).mean()) >= frac_exact, f"only {(ulp == 0).mean():.5f} identical"
+    assert ulp[..., rotary_dim:].max(initial=0) <= 1, "unrotated dimensions beyond 1 ulp"
+    if rotary_dim:
+        af = bf16.to_f32(a[..., :rotary_dim]).astype(np.float64)
+        ef = bf16.to_f32(e[..., :rotary_dim]).astype(np.float64)
+        bound = 2.0 ** -5 * 1.02 * np.abs(ef).max(axis=-1, keepdims=True) + 2.0 ** -7 * np.abs(ef)
+        worst = (np.abs(af - ef) - bound).max()
+        assert worst <= 0, f"rotated output beyond the propagated bound by {worst}"

@@ -13,7 +13,7 @@ import numpy as np
 import pytest
 import torch
 
-from helpers import assert_bf16_close, bf16_randn, from_np, to_np
+from helpers import assert_bf16_close, assert_rope_close, bf16_randn, from_np, to_np
 from oracle import bf16, reference as ref, torch_path as tp
 
 
@@ -270,3 +270,80 @@ def test_swiglu_against_torch():
 def test_golden_fixtures_reproduce():
     import golden_check
     golden_check.check_all(ref)
+
+
+# ------------------------------------------------------ QK norm + RoPE ----
+def _qk_inputs(seed, batch=2, tokens=37, heads=3, dim=128, rot=128):
+    g = gen(seed)
+    q = bf16_randn((batch, tokens, heads, dim), g, outliers=0.01)
+    k = bf16_randn((batch, tokens, heads, dim), g)
+    qw = (1 + 0.1 * torch.randn(dim, generator=g)).bfloat16()
+    kw = (1 + 0.1 * torch.randn(dim, generator=g)).bfloat16()
+    phase = torch.randn(tokens, rot, generator=g) * 3
+    return q, k, qw, kw, phase.cos(), phase.sin()
+
+
+@pytest.mark.parametrize("dim,rot", [(128, 128), (128, 16), (128, 64), (64, 64), (64, 32), (32, 16), (128, 0)])
+def test_qk_norm_rope_close_to_reference_semantics(dim, rot):
+    q, k, qw, kw, cos, sin = _qk_inputs(30 + dim + rot, dim=dim, rot=rot)
+    ours = ref.qk_norm_rope(to_np(q), to_np(k), to_np(qw), to_np(kw), cos.numpy(), sin.numpy(), 1e-6)
+    theirs = tp.qk_norm_rope(q, k, qw, kw, cos, sin, 1e-6)
+    for o, t in zip(ours, theirs):
+        assert_rope_close(o, to_np(t), rot)
+
+
+def test_qk_norm_rope_closed_forms():
+    dim, tokens = 128, 4
+    c = np.where(np.arange(tokens * 2 * dim) % 3 == 0, -0.25, 4.0).astype(np.float32)
+    x = np.repeat(c.reshape(tokens, 2, dim)[:, :, :1], dim, axis=2)[None]  # constant rows of +-2^k
+    x16 = bf16.from_f32(x)
+    ones = bf16.from_f32(np.ones(dim, np.float32))
+    # cos = 1, sin = 0: out = n = sign(row) exactly (rstd = 1/|c| is exact for powers of two)
+    qo, ko = ref.qk_norm_rope(x16, x16, ones, ones, np.ones((tokens, dim), np.float32),
+                              np.zeros((tokens, dim), np.float32), 0.0)
+    assert np.array_equal(bf16.to_f32(qo), np.sign(x)) and np.array_equal(qo, ko)
+    # cos = 0, sin = 1 (a quarter turn): out[:h] = -n[h:], out[h:] = n[:h]
+    g = gen(5)
+    y = to_np(bf16_randn((1, tokens, 2, dim), g))
+    w = to_np((1 + 0.1 * torch.randn(dim, generator=g)).bfloat16())
+    n, _ = ref.qk_norm_rope(y, y, w, w, np.ones((tokens, dim), np.float32), np.zeros((tokens, dim), np.float32), 1e-6)
+    r, _ = ref.qk_norm_rope(y, y, w, w, np.zeros((tokens, dim), np.float32), np.ones((tokens, dim), np.float32), 1e-6)
+    nf, rf = bf16.to_f32(n), bf16.to_f32(r)
+    assert np.array_equal(rf[..., :64], -nf[..., 64:]) and np.array_equal(rf[..., 64:], nf[..., :64])
+    # partial rotary: dimensions past rotary_dim are the normalized row unchanged
+    p, _ = ref.qk_norm_rope(y, y, w, w, np.cos(np.ones((tokens, 16), np.float32)),
+                            np.sin(np.ones((tokens, 16), np.float32)), 1e-6)
+    assert np.array_equal(p[..., 16:], n[..., 16:]) and not np.array_equal(p[..., :16], n[..., :16])
+    # no rotary: the normalized row
+    z, _ = ref.qk_norm_rope(y, y, w, w, np.zeros((tokens, 0), np.float32), np.zeros((tokens, 0), np.float32), 1e-6)
+    assert np.array_equal(z, n)
+
+
+@pytest.mark.parametrize("dim", [128, 64, 32])
+def test_qk_sum_is_exact_when_no_rounding_happens(dim):
+    v = (np.arange(dim) % 9 - 4).astype(np.float32)
+    assert ref.qk_sumsq(bf16.from_f32(v)) == float((v.astype(np.int64) ** 2).sum())
+
+
+@pytest.mark.parametrize("dim,ones,expect", [
+    # A square of 2^24 at element 0 absorbs a lone 1 (2^24 + 1 ties to even),
+    # but not a 2 formed by two 1s that meet first. The reference's ordered
+    # reduction (model/kernels.py:333-344) pairs element i with i + 16 first
+    # inside a 32-element chunk, then i + 8, ..., i + 1:
+    (128, (1, 17), 2.0 ** 24 + 2),    # 1 and 17 meet at the first step
+    (128, (2, 3), 2.0 ** 24),         # 2 and 3 only at the last; absorbed one by one
+    (128, (1, 9), 2.0 ** 24 + 2),     # 1 and 9 meet at the second step
+    # chunk sums (s0, s1, s2, s3) combine as (s0 + s2) + (s1 + s3):
+    (128, (32, 96), 2.0 ** 24 + 2),   # s1 + s3 = 2 before meeting s0
+    (128, (32, 64), 2.0 ** 24),       # s2 joins s0 alone, then s1
+    (64, (2, 3), 2.0 ** 24),
+    (64, (1, 33), 2.0 ** 24),         # chunks first: a flat 64-wide tree would pair 1 with 33
+    (32, (4, 20), 2.0 ** 24 + 2),
+    (32, (4, 5), 2.0 ** 24),
+])
+def test_qk_sum_order(dim, ones, expect):
+    v = np.zeros(dim, np.float32)
+    v[0] = 4096.0
+    v[list(ones)] = 1.0
+    got = ref.qk_sumsq(bf16.from_f32(v))
+    assert got == expect
