@@ -56,6 +56,9 @@ def parse():
     p.add_argument("--ffn", type=int, default=20480)
     p.add_argument("--cpu-tokens", type=int, default=256, help="token slice timed on the CPU")
     p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--workload", choices=("c3", "c4"), default="c3",
+                   help="c3: the projection chain (default, the headline line); c4: the T=65536 W8A8 "
+                        "FFN against the same shapes in bf16 (BASELINE config 4)")
     p.add_argument("--copy-calibration", action="store_true",
                    help="after the timed steps, run a plain 512 MiB device copy three times; under "
                         "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE it scales those counters to bytes")
@@ -221,6 +224,102 @@ def run_cpu(args, data):
             "cpu": _cpu_name()}
 
 
+def run_c4(args):
+    """W8A8 FFN at T=65536 against the same shapes in bf16.
+
+    W8A8 step: quantize_rows(x) -> up GEMM (N=20480) + GELU-tanh epilogue ->
+    quantize_rows(h) -> down GEMM (K=20480, N=5120) + bias.
+    bf16 step: the same weights dequantized to bf16, F.linear (hipBLASLt with
+    its bias epilogue) for both projections, F.gelu(approximate="tanh") between,
+    as an unquantized Linear -> GELU -> Linear feed-forward runs.
+    Returns the JSON line (value = W8A8 GEMM TOPS of the step).
+    """
+    import torch
+    import torch.nn.functional as F
+    from lynnreal_omni_amd import kernels as k
+    from lynnreal_omni_amd.int8_gemm import int8_matmul
+
+    tokens, hidden, ffn = args.tokens, args.hidden, args.ffn
+    g = torch.Generator().manual_seed(20261201 + 3)
+    x = torch.randn(tokens, hidden, generator=g)
+    idx = torch.randperm(hidden, generator=g)[: max(1, round(0.01 * hidden))]
+    x[:, idx] *= 20
+    dev = torch.device("cuda:0")
+    x = x.bfloat16().to(dev)
+    W = {}
+    for name, n, kk in (("up", ffn, hidden), ("down", hidden, ffn)):
+        w = torch.randint(-127, 128, (n, kk), dtype=torch.int8, generator=g)
+        s = torch.rand(n, generator=g) * 4e-3 + 1e-3
+        b = (0.02 * torch.randn(n, generator=g)).bfloat16()
+        W[name] = (w.to(dev), s.to(dev), b.to(dev))
+    wb = {n: (w.float() * s[:, None]).bfloat16() for n, (w, s, _) in W.items()}   # [N, K] bf16
+    torch.cuda.synchronize()
+
+    def w8a8(ev):
+        ev[0].record()
+        q, s = k.quantize_rows(x)
+        ev[1].record()
+        h = int8_matmul(q, W["up"][0].t(), s, W["up"][1], W["up"][2], activation="gelu_tanh")
+        ev[2].record()
+        q3, s3 = k.quantize_rows(h)
+        ev[3].record()
+        y = int8_matmul(q3, W["down"][0].t(), s3, W["down"][1], W["down"][2])
+        ev[4].record()
+        return y
+
+    def bf16(ev):
+        ev[0].record()
+        h = F.linear(x, wb["up"], W["up"][2])
+        ev[1].record()
+        h = F.gelu(h, approximate="tanh")
+        ev[2].record()
+        y = F.linear(h, wb["down"], W["down"][2])
+        ev[3].record()
+        return y
+
+    def timed(fn, marks):
+        for _ in range(args.warmup):
+            fn([torch.cuda.Event() for _ in range(marks)])
+        torch.cuda.synchronize()
+        evs = [[torch.cuda.Event(enable_timing=True) for _ in range(marks)] for _ in range(args.steps)]
+        out = None
+        for ev in evs:
+            out = fn(ev)
+        torch.cuda.synchronize()
+        spans = [[ev[i].elapsed_time(ev[i + 1]) * 1e3 for i in range(marks - 1)] for ev in evs]
+        return out, [statistics.mean(c) for c in zip(*spans)]
+
+    y8, t8 = timed(w8a8, 5)
+    y16, t16 = timed(bf16, 4)
+    a, b = y8.float().reshape(-1), y16.float().reshape(-1)
+    cos = float(torch.dot(a, b) / (a.norm() * b.norm()))
+    ops_up, ops_down = 2 * tokens * hidden * ffn, 2 * tokens * ffn * hidden
+    gemm8_us, gemm16_us = t8[1] + t8[3], t16[0] + t16[2]
+    step8_us, step16_us = sum(t8), sum(t16)
+    log(json.dumps({"w8a8_us": dict(zip(["quant_x", "up_gelu", "quant_h", "down"], t8)),
+                    "bf16_us": dict(zip(["up_bias", "gelu", "down_bias"], t16)),
+                    "cosine_w8a8_vs_bf16": cos}, indent=1))
+    return {
+        "metric": "C4 W8A8 FFN TOPS and speedup over bf16 GEMMs at T=65536",
+        "value": round((ops_up + ops_down) / (gemm8_us * 1e-6) / 1e12, 1),
+        "unit": "TOPS", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(step8_us / 1e3, 3), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "int8", "data": "synthetic (seed 20261201+3), resident in HBM",
+        "config": {"workload": "C4 large-shape FFN", "tokens": tokens, "hidden": hidden, "ffn": ffn,
+                   "ffn_activation": "gelu_tanh", "parallelism": "single GPU"},
+        "gemm_speedup_vs_bf16": round(gemm16_us / gemm8_us, 3),
+        "step_speedup_vs_bf16": round(step16_us / step8_us, 3),
+        "w8a8": {"up_tops": round(ops_up / (t8[1] * 1e-6) / 1e12, 1),
+                 "down_tops": round(ops_down / (t8[3] * 1e-6) / 1e12, 1),
+                 "quant_x_us": round(t8[0], 1), "quant_h_us": round(t8[2], 1),
+                 "step_us": round(step8_us, 1)},
+        "bf16": {"up_tflops": round(ops_up / (t16[0] * 1e-6) / 1e12, 1),
+                 "down_tflops": round(ops_down / (t16[2] * 1e-6) / 1e12, 1),
+                 "gelu_us": round(t16[1], 1), "step_us": round(step16_us, 1)},
+        "cosine_w8a8_vs_bf16": round(cos, 6),
+    }
+
+
 def _cpu_name():
     try:
         for line in open("/proc/cpuinfo"):
@@ -242,6 +341,12 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py needs a GPU", file=sys.stderr)
         return 1
+    if args.workload == "c4":
+        if args.tokens == 12288:
+            args.tokens = 65536
+        log(f"device {torch.cuda.get_device_name(0)}; C4 FFN T={args.tokens} D={args.hidden}")
+        print(json.dumps(run_c4(args)), flush=True)
+        return 0
     log(f"device {torch.cuda.get_device_name(0)}; generating C3 inputs T={args.tokens} D={args.hidden}")
     data = make_inputs(args.tokens, args.hidden, args.ffn, 20261201 + CONFIG_INDEX)
     wall, step_ms, kern_us = run_gpu(args, data)

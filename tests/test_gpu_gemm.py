@@ -159,3 +159,32 @@ def test_empty_and_invalid():
     with pytest.raises(ValueError):
         int8_gemm.int8_matmul(torch.zeros(4, 64, dtype=torch.int8, device="cuda"), b,
                               torch.ones(4, device="cuda"), torch.ones(31, device="cuda"))
+
+
+def test_c4_shapes_beyond_2gib():
+    """BASELINE config 4 shapes (T=65536): FFN-up output bf16 [65536, 20480]
+    (2.7 GB), its per-row quantization (K=20480) and the FFN-down GEMM
+    (K=20480). Rows at the start, middle and end, whose byte offsets pass
+    2^31, are checked against the oracle."""
+    from lynnreal_omni_amd import kernels
+    g = torch.Generator(device="cuda").manual_seed(15)
+    m, d, f = 65536, 5120, 20480
+    a = torch.randint(-127, 128, (m, d), dtype=torch.int8, device="cuda", generator=g)
+    rs = torch.rand(m, device="cuda", generator=g) / 127 + 1e-4
+    w_up = torch.randint(-127, 128, (f, d), dtype=torch.int8, device="cuda", generator=g)
+    cs_up = torch.rand(f, device="cuda", generator=g) * 4e-3 + 1e-3
+    w_dn = torch.randint(-127, 128, (d, f), dtype=torch.int8, device="cuda", generator=g)
+    rows = torch.cat([torch.arange(0, 32), torch.arange(m // 2 - 16, m // 2 + 16), torch.arange(m - 64, m)])
+    rows_d = rows.cuda()
+    y = int8_gemm.int8_matmul(a, w_up.t(), rs, cs_up)
+    assert y.shape == (m, f)
+    a_s, w_up_h = a[rows_d].cpu().numpy(), w_up.cpu().numpy()
+    want_y = ref.dequant(ref.int_mm(a_s, w_up_h), rs[rows_d].cpu().numpy(), cs_up.cpu().numpy())
+    assert np.array_equal(to_np(y[rows_d]), want_y)
+    q, s = kernels.quantize_rows(y)
+    want_q, want_s = ref.quantize_rows(want_y)
+    assert np.array_equal(q[rows_d].cpu().numpy(), want_q)
+    assert np.array_equal(s[rows_d].reshape(-1).cpu().numpy(), want_s)
+    del y
+    acc = int8_gemm.int8_matmul_int32(q, w_dn.t())
+    assert np.array_equal(acc[rows_d].cpu().numpy(), ref.int_mm(want_q, w_dn.cpu().numpy()))
