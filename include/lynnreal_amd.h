@@ -178,8 +178,9 @@ int lr_gelu_tanh(const void* x, void* out, int64_t count, void* stream);
  *   d <  rotary_dim:   out = bf16(bf16(n[d]*c[d]) + bf16(n[d - rotary_dim/2]*s[d]))
  *   d >= rotary_dim:   out = n[d]
  * with c, s = bf16(cos/sin[token, d]) from fp32 [sequence, rotary_dim]. The
- * sum of squares is in 8-element chunks (fma, element order), chunk j in slot
- * j, slots combined by s[i] += s[i + h], h = head_dim/16 .. 1. q/k element
+ * sum of squares follows model/kernels.py:333-344 (_sum128): 32-element
+ * chunks, each reduced by s[i] += s[i + h], h = 16 .. 1, then the chunk sums
+ * by the same tree ((s0 + s2) + (s1 + s3) for 128-wide heads). q/k element
  * (b, t, h, d) is at b*sequence*token_stride + t*token_stride + h*head_stride
  * + d (bf16 elements); q_out/k_out are contiguous [batch, sequence, heads,
  * head_dim]. head_dim in {32, 64, 128}; rotary_dim 0 or 16 * 2^n. */
@@ -188,6 +189,40 @@ int lr_qk_norm_rope(const void* q, const void* k, const void* q_weight, const vo
                     int64_t sequence, int64_t heads, int64_t q_token_stride, int64_t q_head_stride,
                     int64_t k_token_stride, int64_t k_head_stride, int64_t head_dim,
                     int64_t rotary_dim, float eps, void* stream);
+
+/* Row gather. Replaces the index_select calls of Flash token selection at
+ * model/flash.py:71-80 (compress: hidden.index_select(1, keep),
+ * indices.index_select(0, keep), rotary value.index_select(-2, keep),
+ * mask.index_select(-1, keep)):
+ *   dst[o, i, :] = src[o, index[i], :],  o < outer, i < dst_rows,
+ * src [outer, src_rows, row_bytes], dst [outer, dst_rows, row_bytes], any
+ * element type (rows are bytes). Indices must lie in [0, src_rows); others
+ * are clamped into it. */
+int lr_gather_rows(const void* src, const int64_t* index, void* dst, int64_t outer,
+                   int64_t src_rows, int64_t dst_rows, int64_t row_bytes, void* stream);
+
+/* Flash residual restore. Replaces model/flash.py:82-85 (restore):
+ *   out[o, t, c] = bf16(full[o, t, c]
+ *                       + bf16(bf16(current - input)[o, inverse[t], c] * gain))
+ * full, out bf16 [outer, rows, width]; current, input bf16 [outer,
+ * compressed_rows, width]; inverse int64 [rows] in [0, compressed_rows)
+ * (others are clamped). out may alias full. */
+int lr_flash_restore(const void* full, const void* current, const void* input,
+                     const int64_t* inverse, void* out, int64_t outer, int64_t rows,
+                     int64_t compressed_rows, int64_t width, float gain, void* stream);
+
+/* Nearest-anchor map of Flash token selection. Replaces the search loop of
+ * model/flash.py:26-32 (torch.cdist + argmin per 1024 dropped rows): for each
+ * dropped row d, among anchor rows a with positions[a, 0] == positions[d, 0],
+ * the first a of least (h_d - h_a)^2 + (w_d - w_a)^2 (fp32 coordinates,
+ * distance in fp64; no such anchor gives the first anchor), then
+ *   inverse[dropped[i]] = inverse[anchors[a]].
+ * positions fp32 [tokens, 3] (time, h, w); dropped, anchors int64 row numbers
+ * in [0, tokens) (others are clamped); inverse int64 [tokens], updated in
+ * place at the dropped rows. */
+int lr_flash_nearest_anchor(const float* positions, int64_t tokens, const int64_t* dropped,
+                            int64_t n_dropped, const int64_t* anchors, int64_t n_anchors,
+                            int64_t* inverse, void* stream);
 
 #ifdef __cplusplus
 }

@@ -50,6 +50,9 @@ SIGNATURES = {
     "lr_gelu_tanh": [_P, _P, _I64, _P],
     "lr_qk_norm_rope": [_P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64,
                         _I64, _I64, _F32, _P],
+    "lr_gather_rows": [_P, _P, _P, _I64, _I64, _I64, _I64, _P],
+    "lr_flash_restore": [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _F32, _P],
+    "lr_flash_nearest_anchor": [_P, _I64, _P, _I64, _P, _I64, _P, _P],
     "lr_device_supported": [_I32],
     "lr_abi_version": [],
     "lr_gemm_set_group_m": [_I32],

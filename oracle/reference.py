@@ -238,3 +238,59 @@ def canonical_sumsq(row):
 
 def num_threads() -> int:
     return int(load().lro_num_threads())
+
+
+# --------------------------------------------------- Flash token selection ----
+def flash_spatial_layout(positions, tags, stride=2):
+    """model/flash.py:6-33 in numpy: (keep, inverse) as int64 arrays.
+
+    Rows with tag 0 are video. Per spatial axis (1, 2) the sorted distinct
+    coordinates of the video rows are thinned to every stride-th one plus the
+    largest; a video row is kept when both its coordinates survive, any other
+    row always. inverse maps a kept row to its place in keep and a dropped
+    video row to the place of the first kept video row of the same time (fp32
+    coordinates, as positions.float()) at least squared distance over (h, w),
+    computed in float64; a dropped row with no kept row of its time takes the
+    first kept video row (argmin over a row of +inf).
+    """
+    pos = np.asarray(positions)
+    tags = np.asarray(tags)
+    if pos.ndim != 2 or tags.ndim != 1 or pos.shape != (tags.size, 3):
+        raise ValueError("Flash requires a single shared packed layout")
+    video = tags == 0
+    if not video.any():
+        raise ValueError("Flash requires video tokens")
+    on_grid = np.ones(tags.size, bool)
+    for axis in (1, 2):
+        distinct = np.unique(pos[video, axis])
+        survivors = distinct[::stride]
+        if survivors[-1] != distinct[-1]:
+            survivors = np.append(survivors, distinct[-1])
+        on_grid &= np.isin(pos[:, axis], survivors)
+    kept = ~video | on_grid
+    keep = np.flatnonzero(kept).astype(np.int64)
+    inverse = np.zeros(tags.size, np.int64)
+    inverse[keep] = np.arange(keep.size)
+    dropped = np.flatnonzero(video & ~kept)
+    anchors = np.flatnonzero(video & kept)
+    p32 = pos.astype(np.float32)
+    at, ah, aw = p32[anchors, 0], p32[anchors, 1].astype(np.float64), p32[anchors, 2].astype(np.float64)
+    for lo in range(0, dropped.size, 512):
+        rows = dropped[lo:lo + 512]
+        dh = p32[rows, 1].astype(np.float64)[:, None] - ah[None, :]
+        dw = p32[rows, 2].astype(np.float64)[:, None] - aw[None, :]
+        dist = dh * dh + dw * dw
+        dist[p32[rows, 0][:, None] != at[None, :]] = np.inf
+        inverse[rows] = inverse[anchors[np.argmin(dist, axis=1)]]
+    return keep, inverse
+
+
+def flash_restore(full, current, inp, inverse, gain=1.0):
+    """model/flash.py:83-84 with bf16 tensors: every op rounds to bf16 once.
+
+    full [B, T, D], current/inp [B, T', D] (uint16 bf16 patterns), inverse [T].
+    """
+    from . import bf16
+    delta = bf16.round_f32(bf16.to_f32(current) - bf16.to_f32(inp))
+    delta = bf16.round_f32(delta * np.float32(gain))
+    return bf16.from_f32(bf16.to_f32(full) + delta[:, np.asarray(inverse)])
