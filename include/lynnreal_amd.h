@@ -224,6 +224,22 @@ int lr_flash_nearest_anchor(const float* positions, int64_t tokens, const int64_
                             int64_t n_dropped, const int64_t* anchors, int64_t n_anchors,
                             int64_t* inverse, void* stream);
 
+/* adaLN modulation table. Replaces model/fusion.py:68-69 (and
+ * elementwise_fusion.py:8-10): linear(F.silu(temb).to(bf16)), a skinny bf16
+ * GEMM over the time embeddings:
+ *   a = bf16(silu(temb)) (silu(x) = x / (1 + exp(-x)) in fp32; bf16(temb)
+ *       when apply_silu is 0)
+ *   out[m, n] = bf16(sum_k a[m, k] * weight[n, k] + bias[n])
+ * with the fp32 sum in a fixed order: 64 partials, partial l over the
+ * 8-element chunks c = l, l + 64, ... (fma, element order), combined by
+ * s[i] += s[i + h], h = 32 .. 1. temb fp32 or bf16 [rows, in_features];
+ * weight bf16 [out_features, in_features] (nn.Linear layout); bias bf16
+ * [out_features] or NULL; out bf16 [rows, out_features]. in_features a
+ * multiple of 8, at most 8192. */
+int lr_adaln_table(const void* temb, int temb_is_bf16, int apply_silu, const void* weight,
+                   const void* bias, void* out, int64_t rows, int64_t in_features,
+                   int64_t out_features, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

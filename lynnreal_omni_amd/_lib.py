@@ -53,6 +53,7 @@ SIGNATURES = {
     "lr_gather_rows": [_P, _P, _P, _I64, _I64, _I64, _I64, _P],
     "lr_flash_restore": [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _F32, _P],
     "lr_flash_nearest_anchor": [_P, _I64, _P, _I64, _P, _I64, _P, _P],
+    "lr_adaln_table": [_P, _I32, _I32, _P, _P, _P, _I64, _I64, _I64, _P],
     "lr_device_supported": [_I32],
     "lr_abi_version": [],
     "lr_gemm_set_group_m": [_I32],

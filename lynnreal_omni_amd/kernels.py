@@ -19,6 +19,7 @@ Arithmetic (all fp32 with the reference's bf16 rounding points):
   gelu_tanh            bf16(gelu_tanh(x))  (new: the BASELINE FFN activation)
   qk_norm_rope         per-head RMSNorm of Q/K -> bf16, RoPE with bf16 products
                                                               kernels.py:187-257,345-402
+  adaln_table          bf16(bf16(silu(temb)) @ W^T + bias)     fusion.py:68-69
 
 The RMSNorm sum of squares uses one fixed reduction order (documented in
 include/lynnreal_amd.h) and an IEEE 1/sqrt, so the bf16 outputs reproduce a
@@ -248,3 +249,30 @@ def qk_norm_rope(query, key, query_weight, key_weight, rotary_emb, eps):
               k_out.data_ptr(), batch, sequence, heads, query.stride(1), query.stride(2),
               key.stride(1), key.stride(2), head_dim, rotary_dim, float(eps), _lib.stream(query))
     return q_out, k_out
+
+
+def adaln_table(temb, weight, bias=None, *, silu=True):
+    """The adaLN table linear(F.silu(temb).to(bf16)) (model/fusion.py:68-69).
+
+    temb: fp32 or bf16 [..., in_features]; weight: bf16 [out_features,
+    in_features] (nn.Linear.weight); bias: bf16 [out_features] or None.
+    Returns bf16 [rows, out_features], rows = temb.numel() // in_features.
+    silu=False skips the activation (bf16(temb) is used as is).
+    """
+    if temb.dtype not in (torch.float32, torch.bfloat16):
+        raise ValueError(f"temb must be float32 or bfloat16, got {temb.dtype}")
+    weight = _bf16(weight, "weight")
+    _lib.check_device(weight)
+    out_features, in_features = weight.shape
+    if temb.shape[-1] != in_features:
+        raise ValueError(f"temb has {temb.shape[-1]} features, the weight expects {in_features}")
+    temb = temb.reshape(-1, in_features).contiguous()
+    if bias is not None:
+        bias = _bf16(bias.reshape(-1), "bias")
+        if bias.numel() != out_features:
+            raise ValueError(f"bias has {bias.numel()} entries, expected {out_features}")
+    out = torch.empty(temb.shape[0], out_features, device=weight.device, dtype=torch.bfloat16)
+    _lib.call("lr_adaln_table", temb.data_ptr(), int(temb.dtype == torch.bfloat16), int(bool(silu)),
+              weight.data_ptr(), _lib.ptr(bias), out.data_ptr(), temb.shape[0], in_features,
+              out_features, _lib.stream(weight))
+    return out

@@ -370,3 +370,32 @@ int lro_num_threads(void) {
   return 1;
 #endif
 }
+
+/* ------------------------------------------------- adaLN table (GEMM) --- */
+/* model/fusion.py:68-69: table = linear(F.silu(temb).to(bf16)), here from the
+ * activations a = bf16(silu(temb)) [rows, k]. out[m, n] = bf16(s + bias[n]),
+ * s summed in fp32 in the order defined for the gfx950 kernel: 64 lane
+ * partials, lane l over 8-element chunks c = l, l + 64, ... in increasing c
+ * and element order with fmaf (exact bf16 products, one rounding per step),
+ * then s[i] += s[i + h] for h = 32, ..., 1. w is [n, k] row-major bf16. */
+void lro_adaln_table(const uint16_t* a, const uint16_t* w, const uint16_t* bias, int64_t rows,
+                     int64_t n, int64_t k, uint16_t* out) {
+  const int64_t chunks = k / 8;
+#pragma omp parallel for schedule(static)
+  for (int64_t col = 0; col < n; ++col) {
+    for (int64_t m = 0; m < rows; ++m) {
+      float lane[64];
+      for (int l = 0; l < 64; ++l) {
+        float s = 0.0f;
+        for (int64_t c = l; c < chunks; c += 64)
+          for (int64_t e = 8 * c; e < 8 * c + 8; ++e)
+            s = fmaf(bf2f(a[m * k + e]), bf2f(w[col * k + e]), s);
+        lane[l] = s;
+      }
+      for (int h = 32; h >= 1; h /= 2)
+        for (int i = 0; i < h; ++i) lane[i] = lane[i] + lane[i + h];
+      const float b = bias ? bf2f(bias[col]) : 0.0f;
+      out[m * n + col] = f2bf(lane[0] + b);
+    }
+  }
+}

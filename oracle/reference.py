@@ -36,6 +36,7 @@ _SIGS = {
     "lro_qk_norm_rope": ([_P] * 8 + [_I64] * 9 + [_F32], None),
     "lro_qk_sumsq": ([_P, _I64], ctypes.c_float),
     "lro_num_threads": ([], ctypes.c_int),
+    "lro_adaln_table": ([_P, _P, _P, _I64, _I64, _I64, _P], None),
 }
 
 _lib = None
@@ -294,3 +295,17 @@ def flash_restore(full, current, inp, inverse, gain=1.0):
     delta = bf16.round_f32(bf16.to_f32(current) - bf16.to_f32(inp))
     delta = bf16.round_f32(delta * np.float32(gain))
     return bf16.from_f32(bf16.to_f32(full) + delta[:, np.asarray(inverse)])
+
+
+def adaln_table(a, w, bias=None):
+    """model/fusion.py:68-69 from the activations a = bf16(silu(temb)) [rows, k]
+    (bf16 patterns), weight w [n, k], bias [n] or None -> bf16 [rows, n], with
+    the kernel's defined fp32 summation order."""
+    a = _c(a, np.uint16)
+    w = _c(w, np.uint16)
+    rows, k = a.shape
+    n = w.shape[0]
+    out = np.empty((rows, n), np.uint16)
+    b = None if bias is None else _c(bias, np.uint16)
+    load().lro_adaln_table(_p(a), _p(w), None if b is None else _p(b), rows, n, k, _p(out))
+    return out
