@@ -1,24 +1,24 @@
 """bf16 DiT block with only the element-wise fusions (drop-in for the
 reference's model/elementwise_fusion.py).
 
-The block keeps its own normalisation, attention and projections; the two
-residual updates become _gated_residual and the FFN activation _swiglu, both
-gfx950 kernels. Blocks are duck-typed like the reference's H3 block:
-`adaln_proj.linear`, `adaln_proj.hidden_size`, `norm1`, `norm2`, `attn`,
-`ff.net[0].proj`, `ff.net[2]`.
+The block keeps its own normalisation, attention and projections; the adaLN
+table comes from kernels.adaln_table, the two residual updates become
+_gated_residual and the FFN activation _swiglu, all gfx950 kernels. Blocks
+are duck-typed like the reference's H3 block: `adaln_proj.linear`,
+`adaln_proj.hidden_size`, `norm1`, `norm2`, `attn`, `ff.net[0].proj`,
+`ff.net[2]`.
 """
 from __future__ import annotations
 
 from types import MethodType
 
-import torch.nn.functional as F
-
-from .kernels import _gated_residual, _swiglu
+from .kernels import _gated_residual, _swiglu, adaln_table
 
 
 def _modulation_table(block, temb):
+    """linear(F.silu(temb).to(bf16)).view(-1, 6 * hidden) (model/elementwise_fusion.py:8-10)."""
     linear = block.adaln_proj.linear
-    return linear(F.silu(temb).to(linear.weight.dtype)).view(-1, 6 * block.adaln_proj.hidden_size)
+    return adaln_table(temb, linear.weight, linear.bias).view(-1, 6 * block.adaln_proj.hidden_size)
 
 
 def _modulate(normalized, table, indices, shift_slot, scale_slot, width):
