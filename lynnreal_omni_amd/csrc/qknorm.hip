@@ -37,19 +37,9 @@ struct QkArgs {
   const float* sin;
   uint16_t* qo;
   uint16_t* ko;
-  int64_t rows, sequence, heads, q_ts, q_hs, k_ts, k_hs, head_dim, rotary_dim;
+  int64_t tokens, sequence, heads, q_ts, q_hs, k_ts, k_hs, head_dim, rotary_dim;
   float eps;
 };
-
-template <int O>
-__device__ __forceinline__ uint32_t xor_word(uint32_t w) {
-  return __float_as_uint(xor_partner<O>(__uint_as_float(w)));
-}
-
-template <int O>
-__device__ __forceinline__ uint4 xor_chunk(const uint4& v) {
-  return make_uint4(xor_word<O>(v.x), xor_word<O>(v.y), xor_word<O>(v.z), xor_word<O>(v.w));
-}
 
 // n = bf16((x * rstd) * w) for the 8 elements of a chunk, packed.
 __device__ __forceinline__ uint4 normalize8(const uint4& x, const uint4& w, float rstd) {
@@ -88,72 +78,105 @@ __device__ __forceinline__ float sumsq8(const uint4& x) {
   return s;
 }
 
-// out = bf16(bf16(n * c) -/+ bf16(np * s)) over a chunk; `left` picks '-'.
-__device__ __forceinline__ uint4 rotate8(const uint4& n, const uint4& np, const float c[8],
-                                         const float s[8], bool left) {
-  float nf[8], pf[8];
-  unpack8(n, nf);
-  unpack8(np, pf);
+// n = bf16((x * rstd) * w) for the 8 elements of a chunk, as rounded floats.
+__device__ __forceinline__ void normalize8f(const uint4& x, const uint4& w, float rstd, float n[8]) {
+  float wf[8];
+  unpack8(x, n);
+  unpack8(w, wf);
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    const float a = round_bf(nf[e] * c[e]);
-    const float b = round_bf(pf[e] * s[e]);
-    nf[e] = left ? a - b : a + b;
-  }
-  return pack8(nf);
+  for (int e = 0; e < 8; ++e) n[e] = round_bf((n[e] * rstd) * wf[e]);
+}
+
+// The rotary partner's rounded floats, one DPP move each (no pack/unpack).
+template <int D>
+__device__ __forceinline__ void partner8(const float n[8], float np[8]) {
+#pragma unroll
+  for (int e = 0; e < 8; ++e) np[e] = xor_partner<D>(n[e]);
 }
 
 // L lanes per row (head_dim = 8L); D = rotary_dim / 16 (0: no rotary).
+// One wave per token: it loads the token's cos/sin once (rounded to bf16,
+// lanes j < 2D) and walks the token's heads RPW = 64 / L at a time, the next
+// group's Q/K slices in flight while the current group is normalized and
+// rotated. Loads and stores go through buffer descriptors that end at the
+// token's last head, so heads past the end read zero and are not stored
+// without any branch (a conditional memory access would make the compiler
+// wait for every outstanding load).
 template <int L, int D>
 __global__ __launch_bounds__(256) void qk_norm_rope(QkArgs p) {
-  constexpr int RPW = 64 / L;  // rows per wave
+  constexpr int RPW = 64 / L;  // rows (heads) per wave step
   const int lane = threadIdx.x & 63;
-  const int j = lane % L;
-  const int64_t row = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * RPW + lane / L;
-  const bool valid = row < p.rows;
-  const int64_t h = valid ? row % p.heads : 0;
-  const int64_t t = valid ? (row / p.heads) % p.sequence : 0;
-  const int64_t b = valid ? row / (p.heads * p.sequence) : 0;
-
-  uint4 qx = make_uint4(0, 0, 0, 0), kx = qx;
-  if (valid) {
-    qx = *reinterpret_cast<const uint4*>(p.q + b * p.sequence * p.q_ts + t * p.q_ts + h * p.q_hs + 8 * j);
-    kx = *reinterpret_cast<const uint4*>(p.k + b * p.sequence * p.k_ts + t * p.k_ts + h * p.k_hs + 8 * j);
-  }
-  // Every lane takes part in the cross-lane steps; rows past the end hold zeros.
-  const float q_rstd = rsqrt_row(p.eps, p.head_dim, sumsq8<L>(qx));
-  const float k_rstd = rsqrt_row(p.eps, p.head_dim, sumsq8<L>(kx));
+  const int j = lane % L, sub = lane / L;
+  const int64_t token = (int64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  if (token >= p.tokens) return;  // whole wave
+  const int64_t b = token / p.sequence, t = token - b * p.sequence;
+  const auto rq = row_rsrc(p.q + b * p.sequence * p.q_ts + t * p.q_ts, 2 * p.heads * p.q_hs);
+  const auto rk = row_rsrc(p.k + b * p.sequence * p.k_ts + t * p.k_ts, 2 * p.heads * p.k_hs);
+  const auto rqo = row_rsrc(p.qo + token * p.heads * p.head_dim, 2 * p.heads * p.head_dim);
+  const auto rko = row_rsrc(p.ko + token * p.heads * p.head_dim, 2 * p.heads * p.head_dim);
   const uint4 qw = *reinterpret_cast<const uint4*>(p.qw + 8 * j);
   const uint4 kw = *reinterpret_cast<const uint4*>(p.kw + 8 * j);
-  uint4 qn = normalize8(qx, qw, q_rstd);
-  uint4 kn = normalize8(kx, kw, k_rstd);
-  if (D > 0) {
-    const uint4 qp = xor_chunk<D>(qn);
-    const uint4 kp = xor_chunk<D>(kn);
-    if (j < 2 * D && valid) {
-      float c[8], s[8];
-      const float4* cr = reinterpret_cast<const float4*>(p.cos + t * p.rotary_dim + 8 * j);
-      const float4* sr = reinterpret_cast<const float4*>(p.sin + t * p.rotary_dim + 8 * j);
-      const float4 c0 = cr[0], c1 = cr[1], s0 = sr[0], s1 = sr[1];
-      c[0] = c0.x; c[1] = c0.y; c[2] = c0.z; c[3] = c0.w; c[4] = c1.x; c[5] = c1.y; c[6] = c1.z; c[7] = c1.w;
-      s[0] = s0.x; s[1] = s0.y; s[2] = s0.z; s[3] = s0.w; s[4] = s1.x; s[5] = s1.y; s[6] = s1.z; s[7] = s1.w;
+  float c[8], sn[8];
+  if (D > 0 && j < 2 * D) {
+    const float4* cr = reinterpret_cast<const float4*>(p.cos + t * p.rotary_dim + 8 * j);
+    const float4* sr = reinterpret_cast<const float4*>(p.sin + t * p.rotary_dim + 8 * j);
+    const float4 c0 = cr[0], c1 = cr[1], s0 = sr[0], s1 = sr[1];
+    c[0] = c0.x; c[1] = c0.y; c[2] = c0.z; c[3] = c0.w; c[4] = c1.x; c[5] = c1.y; c[6] = c1.z; c[7] = c1.w;
+    sn[0] = s0.x; sn[1] = s0.y; sn[2] = s0.z; sn[3] = s0.w; sn[4] = s1.x; sn[5] = s1.y; sn[6] = s1.z; sn[7] = s1.w;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) c[e] = round_bf(c[e]), s[e] = round_bf(s[e]);
-      const bool left = (j & D) == 0;
-      qn = rotate8(qn, qp, c, s, left);
-      kn = rotate8(kn, kp, c, s, left);
-    }
+    for (int e = 0; e < 8; ++e) c[e] = round_bf(c[e]), sn[e] = round_bf(sn[e]);
   }
-  if (valid) {
-    *reinterpret_cast<uint4*>(p.qo + row * p.head_dim + 8 * j) = qn;
-    *reinterpret_cast<uint4*>(p.ko + row * p.head_dim + 8 * j) = kn;
+  // Byte offsets inside the token (the descriptors end at head `heads`).
+  const uint32_t q_step = (uint32_t)(2 * RPW * p.q_hs), k_step = (uint32_t)(2 * RPW * p.k_hs);
+  const uint32_t o_step = (uint32_t)(2 * RPW * p.head_dim);
+  uint32_t q_off = (uint32_t)(2 * (sub * p.q_hs + 8 * j));
+  uint32_t k_off = (uint32_t)(2 * (sub * p.k_hs + 8 * j));
+  uint32_t o_off = (uint32_t)(2 * (sub * p.head_dim + 8 * j));
+  uint4 qx = buf_load16(rq, q_off), kx = buf_load16(rk, k_off);
+  for (int64_t h0 = 0; h0 < p.heads; h0 += RPW) {
+    q_off += q_step;
+    k_off += k_step;
+    // The next group (zeros past the last head).
+    const uint4 qn_x = buf_load16(rq, q_off), kn_x = buf_load16(rk, k_off);
+    // Every lane takes part in the cross-lane steps; heads past the end hold zeros.
+    const float q_rstd = rsqrt_row(p.eps, p.head_dim, sumsq8<L>(qx));
+    const float k_rstd = rsqrt_row(p.eps, p.head_dim, sumsq8<L>(kx));
+    uint4 qn, kn;
+    if (D == 0) {
+      qn = normalize8(qx, qw, q_rstd);
+      kn = normalize8(kx, kw, k_rstd);
+    } else {
+      // Rounded floats throughout: the partner comes over DPP as floats, so
+      // nothing is packed and unpacked again before the rotation.
+      float nq[8], nk[8], pq[8], pk[8];
+      normalize8f(qx, qw, q_rstd, nq);
+      normalize8f(kx, kw, k_rstd, nk);
+      partner8<D>(nq, pq);
+      partner8<D>(nk, pk);
+      if (j < 2 * D) {
+        const bool left = (j & D) == 0;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float aq = round_bf(nq[e] * c[e]), bq = round_bf(pq[e] * sn[e]);
+          const float ak = round_bf(nk[e] * c[e]), bk = round_bf(pk[e] * sn[e]);
+          nq[e] = left ? aq - bq : aq + bq;
+          nk[e] = left ? ak - bk : ak + bk;
+        }
+      }
+      qn = pack8(nq);
+      kn = pack8(nk);
+    }
+    buf_store16(rqo, o_off, 0, qn);
+    buf_store16(rko, o_off, 0, kn);
+    o_off += o_step;
+    qx = qn_x;
+    kx = kn_x;
   }
 }
 
 template <int L, int D>
 void launch(const QkArgs& p, hipStream_t st) {
-  const int64_t rows_per_block = 4 * (64 / L);
-  const int64_t blocks = (p.rows + rows_per_block - 1) / rows_per_block;
+  const int64_t blocks = (p.tokens + 3) / 4;
   hipLaunchKernelGGL((qk_norm_rope<L, D>), dim3((unsigned)blocks), dim3(256), 0, st, p);
 }
 
@@ -204,12 +227,18 @@ extern "C" int lr_qk_norm_rope(const void* q, const void* k, const void* q_weigh
                           (rotary_dim == 0 || (aligned(cos, 16) && aligned(sin, 16)));
   if (!aligned_ok)
     return fail(LR_EUNSUPPORTED, "qk_norm_rope: rows must be 16-byte aligned");
-  LR_REQUIRE(rows / (4 * (64 / (head_dim / 8))) < 0x7fffffffLL, "qk_norm_rope: too many rows");
+  LR_REQUIRE((batch * sequence + 3) / 4 < 0x7fffffffLL, "qk_norm_rope: too many tokens");
+  // Per-token descriptors: a token's heads must span less than 2^31 bytes.
+  LR_REQUIRE(heads * (q_head_stride > k_head_stride ? q_head_stride : k_head_stride) <
+                 (1LL << 30) - 64 * head_dim,
+             "qk_norm_rope: a token's heads span too many bytes");
+  LR_REQUIRE(q_head_stride >= head_dim && k_head_stride >= head_dim,
+             "qk_norm_rope: heads must not overlap (head stride < head_dim)");
   QkArgs p{};
   p.q = (const uint16_t*)q; p.k = (const uint16_t*)k;
   p.qw = (const uint16_t*)q_weight; p.kw = (const uint16_t*)k_weight;
   p.cos = cos; p.sin = sin; p.qo = (uint16_t*)q_out; p.ko = (uint16_t*)k_out;
-  p.rows = rows; p.sequence = sequence; p.heads = heads;
+  p.tokens = batch * sequence; p.sequence = sequence; p.heads = heads;
   p.q_ts = q_token_stride; p.q_hs = q_head_stride; p.k_ts = k_token_stride; p.k_hs = k_head_stride;
   p.head_dim = head_dim; p.rotary_dim = rotary_dim; p.eps = eps;
   hipStream_t st = as_stream(stream);
