@@ -188,3 +188,22 @@ def test_c4_shapes_beyond_2gib():
     del y
     acc = int8_gemm.int8_matmul_int32(q, w_dn.t())
     assert np.array_equal(acc[rows_d].cpu().numpy(), ref.int_mm(want_q, w_dn.cpu().numpy()))
+
+
+def test_int8_tma_entry_matches_int8_matmul():
+    """model/int8_tma.py:33-41's entry point: same output as int8_matmul, and
+    the reference's tile tuples map onto HIP tiles."""
+    from lynnreal_omni_amd import int8_tma
+    g = gen(16)
+    m, n, k = 1024, 768, 1024
+    a = torch.randint(-127, 128, (m, k), dtype=torch.int8, generator=g).cuda()
+    w = torch.randint(-127, 128, (n, k), dtype=torch.int8, generator=g).cuda()
+    rs = (torch.rand(m, 1, generator=g) / 127).cuda()
+    cs = (torch.rand(1, n, generator=g) * 4e-3 + 1e-3).cuda()
+    bias = (0.02 * torch.randn(n, generator=g)).bfloat16().cuda()
+    y = int8_tma.matmul(a, w.t(), rs, cs, bias)
+    assert torch.equal(y, int8_gemm.int8_matmul(a, w.t(), rs, cs, bias))
+    assert torch.equal(int8_tma.matmul(a, w.t(), rs, cs, bias, tile=(128, 128, 128, 8, 3)), y)
+    want = ref.dequant(ref.int_mm(a.cpu().numpy(), w.cpu().numpy()), rs.cpu().numpy(), cs.cpu().numpy(),
+                       to_np(bias))
+    assert np.array_equal(to_np(y), want)

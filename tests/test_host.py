@@ -148,3 +148,14 @@ def test_optional_kernel_failure():
     assert not ok(RuntimeError("illegal memory access"))
     assert not ok(ValueError("bad shape"))
     assert not ok(torch.cuda.OutOfMemoryError("not supported"))
+
+
+def test_int8_tma_entry_checks_layout():
+    from lynnreal_omni_amd import int8_tma
+    a = torch.zeros(4, 64, dtype=torch.int8)
+    w = torch.zeros(32, 64, dtype=torch.int8)
+    s = torch.ones(4)
+    with pytest.raises(ValueError, match="TMA requires"):
+        int8_tma.matmul(a, w.t().contiguous(), s, torch.ones(32))      # stride (32, 1), not (1, K)
+    with pytest.raises(ValueError, match="TMA requires"):
+        int8_tma.matmul(a.float(), w.t(), s, torch.ones(32))
