@@ -433,10 +433,17 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_fast(GemmArgs p) 
     const char* sb = b_ring + (kt % NB) * B_BYTES;
     const int kt_b = kt + NB - 1, kt_a = kt + NA - 1;
     v4i a0[FM], w0[FN], a1[FM], w1[FN];
+    // Read in MFMA order (a0[0], then the W fragments, then a0[1..]): the
+    // first MFMA waits for two reads, not for all of them, while every wave
+    // of the block is reading at once right after the barrier.
+    a0[0] = frag(sa, wm * FM, 0);
 #pragma unroll
-    for (int j = 0; j < FN; ++j) w0[j] = frag(sb, wn * FN + j, 0);
+    for (int j = 0; j < FN; ++j) {
+      w0[j] = frag(sb, wn * FN + j, 0);
+      __builtin_amdgcn_sched_barrier(0);
+    }
 #pragma unroll
-    for (int i = 0; i < FM; ++i) a0[i] = frag(sa, wm * FM + i, 0);
+    for (int i = 1; i < FM; ++i) a0[i] = frag(sa, wm * FM + i, 0);
     __builtin_amdgcn_sched_barrier(0);
 #if GEMM_SETPRIO
     __builtin_amdgcn_s_setprio(1);
