@@ -183,7 +183,7 @@ int lr_gelu_tanh(const void* x, void* out, int64_t count, void* stream);
  * by the same tree ((s0 + s2) + (s1 + s3) for 128-wide heads). q/k element
  * (b, t, h, d) is at b*sequence*token_stride + t*token_stride + h*head_stride
  * + d (bf16 elements); q_out/k_out are contiguous [batch, sequence, heads,
- * head_dim]. head_dim in {32, 64, 128}; rotary_dim 0 or 16 * 2^n. */
+ * head_dim]. head_dim in {32, 64, 128}; rotary_dim a multiple of 16 (0 included). */
 int lr_qk_norm_rope(const void* q, const void* k, const void* q_weight, const void* k_weight,
                     const float* cos, const float* sin, void* q_out, void* k_out, int64_t batch,
                     int64_t sequence, int64_t heads, int64_t q_token_stride, int64_t q_head_stride,

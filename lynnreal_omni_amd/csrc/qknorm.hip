@@ -20,8 +20,8 @@
 // holds elements 32c + 8a + e, e < 8, so h = 16 and 8 pair lanes a ^ 2 and
 // a ^ 1 element by element (DPP), h = 4, 2, 1 stay inside the lane, and the
 // chunk tree pairs lanes j ^ 8 and j ^ 4. The rotary partner of chunk j is
-// chunk j ^ (rotary_dim / 16), fetched from that lane with DPP, so Q and K
-// are each read once.
+// chunk j + D or j - D (D = rotary_dim / 16), fetched from that lane with
+// DPP, so Q and K are each read once.
 #include "lr_device.h"
 #include "lr_runtime.h"
 
@@ -87,11 +87,28 @@ __device__ __forceinline__ void normalize8f(const uint4& x, const uint4& w, floa
   for (int e = 0; e < 8; ++e) n[e] = round_bf((n[e] * rstd) * wf[e]);
 }
 
-// The rotary partner's rounded floats, one DPP move each (no pack/unpack).
+// The rotary partner's rounded floats (no pack/unpack): chunk j < D pairs
+// with chunk j + D, chunk j in [D, 2D) with j - D. A power-of-two D is the
+// lane XOR j ^ D (DPP); any other D < 16 is a row shift of D lanes, down for
+// the first half and up for the second (DPP row_shl / row_shr, which stay in
+// the 16-lane row: j + D < 2D <= L <= 16 and j - D >= 0).
 template <int D>
-__device__ __forceinline__ void partner8(const float n[8], float np[8]) {
+__device__ __forceinline__ float row_shift_partner(float v, bool first_half) {
+  static_assert(D > 0 && D < 16, "row shift distance");
+  const int u = __float_as_int(v);
+  const int down = __builtin_amdgcn_mov_dpp(u, 0x100 + D, 0xf, 0xf, false);  // lane i <- i + D
+  const int up = __builtin_amdgcn_mov_dpp(u, 0x110 + D, 0xf, 0xf, false);    // lane i <- i - D
+  return __int_as_float(first_half ? down : up);
+}
+
+template <int D>
+__device__ __forceinline__ void partner8(const float n[8], float np[8], bool first_half) {
+  constexpr bool kXor = (D & (D - 1)) == 0;
 #pragma unroll
-  for (int e = 0; e < 8; ++e) np[e] = xor_partner<D>(n[e]);
+  for (int e = 0; e < 8; ++e) {
+    if constexpr (kXor) np[e] = xor_partner<D>(n[e]);
+    else np[e] = row_shift_partner<D>(n[e], first_half);
+  }
 }
 
 // L lanes per row (head_dim = 8L); D = rotary_dim / 16 (0: no rotary).
@@ -151,10 +168,10 @@ __global__ __launch_bounds__(256) void qk_norm_rope(QkArgs p) {
       float nq[8], nk[8], pq[8], pk[8];
       normalize8f(qx, qw, q_rstd, nq);
       normalize8f(kx, kw, k_rstd, nk);
-      partner8<D>(nq, pq);
-      partner8<D>(nk, pk);
+      const bool left = j < D;  // first half of the rotary dims: out = a - b
+      partner8<D>(nq, pq, left);
+      partner8<D>(nk, pk, left);
       if (j < 2 * D) {
-        const bool left = (j & D) == 0;
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
           const float aq = round_bf(nq[e] * c[e]), bq = round_bf(pq[e] * sn[e]);
@@ -182,12 +199,16 @@ void launch(const QkArgs& p, hipStream_t st) {
 
 template <int L>
 int launch_rot(const QkArgs& p, hipStream_t st) {
-  // rotary_dim <= head_dim = 8L keeps the pair distance D = rotary_dim / 16 below L.
+  // rotary_dim <= head_dim = 8L keeps the pair distance D = rotary_dim / 16 at most L / 2.
   switch (p.rotary_dim / 16) {
     case 0: launch<L, 0>(p, st); break;
     case 1: launch<L, 1>(p, st); break;
-    case 2: if constexpr (L >= 4) launch<L, 2>(p, st); break;
+    case 2: launch<L, 2>(p, st); break;
+    case 3: if constexpr (L >= 8) launch<L, 3>(p, st); break;
     case 4: if constexpr (L >= 8) launch<L, 4>(p, st); break;
+    case 5: if constexpr (L >= 16) launch<L, 5>(p, st); break;
+    case 6: if constexpr (L >= 16) launch<L, 6>(p, st); break;
+    case 7: if constexpr (L >= 16) launch<L, 7>(p, st); break;
     case 8: if constexpr (L >= 16) launch<L, 8>(p, st); break;
     default: return fail(LR_EUNSUPPORTED, "qk_norm_rope: rotary_dim %lld not supported",
                          (long long)p.rotary_dim);
@@ -216,9 +237,8 @@ extern "C" int lr_qk_norm_rope(const void* q, const void* k, const void* q_weigh
   if (!(head_dim == 32 || head_dim == 64 || head_dim == 128))
     return fail(LR_EUNSUPPORTED, "qk_norm_rope: head_dim %lld not supported (32, 64, 128)",
                 (long long)head_dim);
-  const int64_t r16 = rotary_dim / 16;
-  if (rotary_dim % 16 != 0 || (r16 & (r16 - 1)) != 0)
-    return fail(LR_EUNSUPPORTED, "qk_norm_rope: rotary_dim %lld not supported (0 or 16 * 2^n)",
+  if (rotary_dim % 16 != 0)
+    return fail(LR_EUNSUPPORTED, "qk_norm_rope: rotary_dim %lld not supported (a multiple of 16)",
                 (long long)rotary_dim);
   const bool aligned_ok = aligned(q, 16) && aligned(k, 16) && aligned(q_weight, 16) &&
                           aligned(k_weight, 16) && aligned(q_out, 16) && aligned(k_out, 16) &&

@@ -25,6 +25,11 @@ CASES = [
     (2, 31, 5, 64, 32),
     (1, 50, 6, 32, 16),
     (1, 19, 3, 128, 0),      # RMSNorm only
+    (1, 33, 5, 128, 48),     # pair distances that are not powers of two: DPP row shifts
+    (2, 21, 3, 128, 80),
+    (1, 40, 4, 128, 96),
+    (1, 17, 6, 128, 112),
+    (1, 29, 7, 64, 48),
 ]
 
 
@@ -73,6 +78,11 @@ def test_qk_norm_rope_rejects_bad_arguments():
     big = torch.zeros(4, 256, device="cuda")
     with pytest.raises(ValueError):
         kernels.qk_norm_rope(q, q, w, w, (big, big), 1e-6)
-    r24 = torch.zeros(4, 24, device="cuda")
+    r24 = torch.zeros(4, 24, device="cuda")          # not a multiple of 16
     with pytest.raises(RuntimeError, match="not supported"):
         kernels.qk_norm_rope(q, q, w, w, (r24, r24), 1e-6)
+    q96 = torch.zeros(1, 4, 2, 96, dtype=torch.bfloat16, device="cuda")
+    w96 = torch.ones(96, dtype=torch.bfloat16, device="cuda")
+    r48 = torch.zeros(4, 48, device="cuda")          # head_dim 96: not a supported width
+    with pytest.raises(RuntimeError, match="not supported"):
+        kernels.qk_norm_rope(q96, q96, w96, w96, (r48, r48), 1e-6)

@@ -283,7 +283,8 @@ def _qk_inputs(seed, batch=2, tokens=37, heads=3, dim=128, rot=128):
     return q, k, qw, kw, phase.cos(), phase.sin()
 
 
-@pytest.mark.parametrize("dim,rot", [(128, 128), (128, 16), (128, 64), (64, 64), (64, 32), (32, 16), (128, 0)])
+@pytest.mark.parametrize("dim,rot", [(128, 128), (128, 16), (128, 64), (64, 64), (64, 32), (32, 16), (128, 0),
+                                     (128, 48), (128, 112), (64, 48)])
 def test_qk_norm_rope_close_to_reference_semantics(dim, rot):
     q, k, qw, kw, cos, sin = _qk_inputs(30 + dim + rot, dim=dim, rot=rot)
     ours = ref.qk_norm_rope(to_np(q), to_np(k), to_np(qw), to_np(kw), cos.numpy(), sin.numpy(), 1e-6)
