@@ -207,3 +207,27 @@ def test_int8_tma_entry_matches_int8_matmul():
     want = ref.dequant(ref.int_mm(a.cpu().numpy(), w.cpu().numpy()), rs.cpu().numpy(), cs.cpu().numpy(),
                        to_np(bias))
     assert np.array_equal(to_np(y), want)
+
+
+@pytest.mark.parametrize("act", [None, "gelu_tanh", "swiglu"])
+def test_chunked_rows_equal_unchunked(act):
+    """Row independence, as the reference's sampling-safety check demands
+    (comfyui/.../tools/verify_sampling_safety.py:58-78: chunked == unchunked
+    for act in none/swiglu/gelu_tanh): the quantized projection of a row
+    block equals the same rows of the whole-batch result, bit for bit."""
+    from lynnreal_omni_amd import kernels
+    g = gen(17)
+    m, n, k = 777, 1024, 512
+    x = bf16_randn((m, k), g, outliers=0.01).cuda()
+    w = torch.randint(-127, 128, (n, k), dtype=torch.int8, generator=g).cuda()
+    cs = (torch.rand(n, generator=g) * 4e-3 + 1e-3).cuda()
+    bias = (0.02 * torch.randn(n, generator=g)).bfloat16().cuda()
+
+    def project(rows):
+        q, s = kernels.quantize_rows(rows)
+        y = int8_gemm.int8_matmul(q, w.t(), s, cs, bias, activation="gelu_tanh" if act == "gelu_tanh" else None)
+        return kernels._swiglu(y) if act == "swiglu" else y
+
+    whole = project(x)
+    parts = torch.cat([project(x[i:i + 100].contiguous()) for i in range(0, m, 100)])
+    assert torch.equal(whole, parts)
