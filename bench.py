@@ -59,6 +59,8 @@ def parse():
     p.add_argument("--workload", choices=("c3", "c4"), default="c3",
                    help="c3: the projection chain (default, the headline line); c4: the T=65536 W8A8 "
                         "FFN against the same shapes in bf16 (BASELINE config 4)")
+    p.add_argument("--no-vendor-gemm", dest="vendor_gemm", action="store_false",
+                   help="skip the like-for-like FFN-up GEMM comparison with torch._int_mm (hipBLASLt)")
     p.add_argument("--copy-calibration", action="store_true",
                    help="after the timed steps, run a plain 512 MiB device copy three times; under "
                         "rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE it scales those counters to bytes")
@@ -185,7 +187,46 @@ def run_gpu(args, data):
         for i, n in enumerate(names):
             per_kernel[n].append(ev[i].elapsed_time(ev[i + 1]))
         step_ms.append(ev[0].elapsed_time(ev[8]))
-    return wall, step_ms, {n: statistics.mean(v) * 1e3 for n, v in per_kernel.items()}
+    kern = {n: statistics.mean(v) * 1e3 for n, v in per_kernel.items()}
+    vendor = None
+    if args.vendor_gemm:
+        vendor = vendor_comparison(args, q2_for_vendor(k, x, norm1, table, idx), W["up"][0])
+    return wall, step_ms, kern, vendor
+
+
+def q2_for_vendor(k, x, norm, table, idx):
+    """The FFN-up GEMM's A operand of the bench data (int8 rows of the modulated input)."""
+    q, _ = k._rms_adaln_quant_int8(x, norm, table, idx, 3, 4)
+    return q
+
+
+def vendor_comparison(args, a, w_kn, reps=10):
+    """The FFN-up shape's raw int32 product on this library and on torch._int_mm
+    (hipBLASLt's INT8 GEMM on ROCm), same operands, same int32 output: a
+    like-for-like check of the GEMM against the vendor library."""
+    import torch
+    from lynnreal_omni_amd.int8_gemm import int8_matmul_int32
+
+    def timed(fn):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(reps):
+            fn()
+        stop.record()
+        stop.synchronize()
+        return start.elapsed_time(stop) * 1e3 / reps
+
+    ours = timed(lambda: int8_matmul_int32(a, w_kn))
+    theirs = timed(lambda: torch._int_mm(a, w_kn))
+    equal = bool(torch.equal(int8_matmul_int32(a, w_kn), torch._int_mm(a, w_kn)))
+    ops = 2 * a.shape[0] * a.shape[1] * w_kn.shape[1]
+    return {"shape": [a.shape[0], w_kn.shape[1], a.shape[1]], "int32_out": True,
+            "ours_us": round(ours, 1), "ours_tops": round(ops / ours / 1e6, 1),
+            "hipblaslt_int_mm_us": round(theirs, 1), "hipblaslt_tops": round(ops / theirs / 1e6, 1),
+            "outputs_equal": equal}
 
 
 def run_cpu(args, data):
@@ -349,7 +390,7 @@ def main():
         return 0
     log(f"device {torch.cuda.get_device_name(0)}; generating C3 inputs T={args.tokens} D={args.hidden}")
     data = make_inputs(args.tokens, args.hidden, args.ffn, 20261201 + CONFIG_INDEX)
-    wall, step_ms, kern_us = run_gpu(args, data)
+    wall, step_ms, kern_us, vendor = run_gpu(args, data)
     if args.copy_calibration:
         # An elementwise kernel (not a DMA-engine memcpy) reading and writing
         # COPY_CALIBRATION_BYTES each, so that it shows up as a dispatch.
@@ -403,6 +444,7 @@ def main():
                      "unit": "TFLOP/s", "frac": round(up_tops / PEAK_INT8_TOPS, 4),
                      "traffic": traffic_bytes("up"), "us": round(up_us, 2)},
         "cpu_baseline": cpu,
+        "vendor_int8_gemm": vendor,
     }
     print(json.dumps(line), flush=True)
     return 0
