@@ -1,7 +1,7 @@
 #!/usr/bin/env python3
 """Benchmark of the W8A8 DiT projection path on one MI355X.
 
-One step = the Flash-block projection chain of BASELINE config 3 at T=12288
+One step = the Flash-block projection chain (benchmark config 3) at T=12288
 tokens, D=5120 (40 heads x 128), FFN 20480 with GELU-tanh, attention output
 replaced by random bf16:
 
@@ -10,7 +10,7 @@ replaced by random bf16:
   FFN-up GEMM (N=20480) + GELU-tanh -> quantize -> FFN-down GEMM (K=20480,
   N=5120) + gated residual (slot 5)
 
-Inputs are synthetic (torch.Generator seeded with
+Inputs are synthetic (the benchmark's own generators: torch.Generator seeded with
 20261201 + config index, N(0,1) activations with 1% outlier channels x20,
 int8 weights uniform in [-127,127], per-channel scales U(1e-3,5e-3), bias
 N(0,0.02)) and resident in HBM before timing. Every kernel of every timed
@@ -58,7 +58,7 @@ def parse():
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--workload", choices=("c3", "c4"), default="c3",
                    help="c3: the projection chain (default, the headline line); c4: the T=65536 W8A8 "
-                        "FFN against the same shapes in bf16 (BASELINE config 4)")
+                        "FFN against the same shapes in bf16 (benchmark config 4)")
     p.add_argument("--no-vendor-gemm", dest="vendor_gemm", action="store_false",
                    help="skip the like-for-like FFN-up GEMM comparison with torch._int_mm (hipBLASLt)")
     p.add_argument("--copy-calibration", action="store_true",
@@ -266,7 +266,7 @@ def run_cpu(args, data):
 
 
 def run_c4(args):
-    """W8A8 FFN at T=65536 against the same shapes in bf16.
+    """Benchmark config 4: W8A8 FFN at T=65536 against the same shapes in bf16.
 
     W8A8 step: quantize_rows(x) -> up GEMM (N=20480) + GELU-tanh epilogue ->
     quantize_rows(h) -> down GEMM (K=20480, N=5120) + bias.
@@ -375,7 +375,7 @@ def main():
     args = parse()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: --gpus {args.gpus} is not supported in this build "
-              "(the projection path shards by tokens with no exchange; see DESIGN.md)",
+              "(the projection path shards by tokens with no exchange between GPUs)",
               file=sys.stderr)
         return 2
     import torch
@@ -430,7 +430,7 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "int8",
-        "data": "synthetic (BASELINE.md section 4 generators, seed 20261201+2), resident in HBM",
+        "data": "synthetic (N(0,1) activations with 1% outlier channels x20, uniform int8 weights, seed 20261201+2), resident in HBM",
         "config": {"workload": "C3 Flash-block W8A8 projection chain", "tokens": args.tokens,
                    "hidden": args.hidden, "heads": "40x128", "ffn": args.ffn,
                    "ffn_activation": "gelu_tanh", "gemm_ops_per_step": total_ops,

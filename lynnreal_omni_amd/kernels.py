@@ -16,7 +16,7 @@ Arithmetic (all fp32 with the reference's bf16 rounding points):
                                                               kernels.py:405-419
   _gated_residual      bf16(x + bf16(gate*u))                 kernels.py:131-153
   _swiglu(_quant)      bf16(v * bf16(g*sigmoid(g))) (-> INT8)  kernels.py:156-185
-  gelu_tanh            bf16(gelu_tanh(x))  (new: the BASELINE FFN activation)
+  gelu_tanh            bf16(gelu_tanh(x))  (new: the benchmark FFN activation)
   qk_norm_rope         per-head RMSNorm of Q/K -> bf16, RoPE with bf16 products
                                                               kernels.py:187-257,345-402
   adaln_table          bf16(bf16(silu(temb)) @ W^T + bias)     fusion.py:68-69

@@ -162,7 +162,7 @@ def test_empty_and_invalid():
 
 
 def test_c4_shapes_beyond_2gib():
-    """BASELINE config 4 shapes (T=65536): FFN-up output bf16 [65536, 20480]
+    """Benchmark config 4 shapes (T=65536): FFN-up output bf16 [65536, 20480]
     (2.7 GB), its per-row quantization (K=20480) and the FFN-down GEMM
     (K=20480). Rows at the start, middle and end, whose byte offsets pass
     2^31, are checked against the oracle."""

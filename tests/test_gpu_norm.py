@@ -86,7 +86,7 @@ def test_rms_adaln_close_to_reference_triton_semantics():
 
 
 def test_full_size_c2_prologue():
-    """T=12288, D=5120: bit-exact against the oracle."""
+    """T=12288, D=5120 (benchmark config 2): bit-exact against the oracle."""
     x, u, w, table, idx = case(1, 12288, 5120, 1, 8)
     q, s = gpu.rms_adaln_quant(x, w, table, idx, 0, 1, 1e-6)
     rq, rs = ref.rms_adaln_quant(x, w, table, idx, 0, 1, 1e-6)
@@ -94,7 +94,7 @@ def test_full_size_c2_prologue():
 
 
 def test_ragged_c5_per_token_modulation():
-    """T=12288+317 with per-frame modulation rows."""
+    """T=12288+317 with per-frame modulation rows (benchmark config 5)."""
     x, u, w, table, idx = case(1, 12605, 5120, 6, 9, True)
     res, q, s = gpu.residual_rms_quant(x, u, w, table, idx, 1e-6)
     rr, rq, rs = ref.residual_rms_quant(x, u, w, table, idx, 1e-6)
