@@ -56,9 +56,11 @@ def parse():
     p.add_argument("--ffn", type=int, default=20480)
     p.add_argument("--cpu-tokens", type=int, default=256, help="token slice timed on the CPU")
     p.add_argument("--no-cpu-baseline", action="store_true")
-    p.add_argument("--workload", choices=("c3", "c4"), default="c3",
-                   help="c3: the projection chain (default, the headline line); c4: the T=65536 W8A8 "
-                        "FFN against the same shapes in bf16 (benchmark config 4)")
+    p.add_argument("--workload", choices=("c3", "c1", "c4", "c5"), default="c3",
+                   help="c3: the projection chain (default, the headline line); c1: one W8A8 linear "
+                        "(2048x5120 -> 5120) with the CPU torch path beside it; c4: the T=65536 W8A8 FFN "
+                        "against the same shapes in bf16; c5: the chain at T=12288+317 with per-frame "
+                        "modulation rows, and M=256 projections")
     p.add_argument("--no-vendor-gemm", dest="vendor_gemm", action="store_false",
                    help="skip the like-for-like FFN-up GEMM comparison with torch._int_mm (hipBLASLt)")
     p.add_argument("--copy-calibration", action="store_true",
@@ -265,6 +267,115 @@ def run_cpu(args, data):
             "cpu": _cpu_name()}
 
 
+def _event_time(fn, reps):
+    import torch
+    for _ in range(3):
+        fn()
+    torch.cuda.synchronize()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(reps):
+        fn()
+    stop.record()
+    stop.synchronize()
+    return start.elapsed_time(stop) * 1e3 / reps
+
+
+def run_c1(args):
+    """Benchmark config 1: one W8A8 linear, X bf16 [2048, 5120] (1% outlier
+    channels x20) -> quantize_rows -> INT8 GEMM (N=5120) + bias -> bf16, and the
+    same computation in torch CPU ops on the host cores (the whole config)."""
+    import torch
+    from lynnreal_omni_amd import kernels as k
+    from lynnreal_omni_amd.int8_gemm import int8_matmul
+    from oracle import torch_path as tp
+
+    m, kk, n = 2048, 5120, 5120
+    g = torch.Generator().manual_seed(20261201 + 0)
+    x = torch.randn(m, kk, generator=g)
+    x[:, torch.randperm(kk, generator=g)[: round(0.01 * kk)]] *= 20
+    x = x.bfloat16()
+    w = torch.randint(-127, 128, (n, kk), dtype=torch.int8, generator=g)
+    s = torch.rand(n, generator=g) * 4e-3 + 1e-3
+    b = (0.02 * torch.randn(n, generator=g)).bfloat16()
+    xd, wd, sd, bd = x.cuda(), w.cuda().t(), s.cuda(), b.cuda()
+
+    def step():
+        q, qs = k.quantize_rows(xd)
+        return int8_matmul(q, wd, qs, sd, bd)
+
+    us = _event_time(step, max(args.steps, 20))
+    y = step()
+    q_t, s_t = tp.quantize(x)
+    want = tp.epilogue(tp.int_mm(q_t, w), s_t, s.reshape(1, -1), b)
+    exact = bool(torch.equal(y.cpu(), want))
+    cores = len(os.sched_getaffinity(0))
+    threads = max(1, min(cores, int(os.environ.get("OMP_NUM_THREADS", cores) or cores)))
+    torch.set_num_threads(threads)
+    times = []
+    for _ in range(3):
+        t = time.perf_counter()
+        q_t, s_t = tp.quantize(x)
+        tp.epilogue(tp.int_mm(q_t, w), s_t, s.reshape(1, -1), b)
+        times.append(time.perf_counter() - t)
+    cpu_s = statistics.median(times)
+    ops = 2 * m * n * kk
+    return {"metric": "C1 W8A8 linear TOPS", "value": round(ops / (us * 1e-6) / 1e12, 1), "unit": "TOPS",
+            "n_gpus": 1, "steps": max(args.steps, 20), "warmup": 3, "ms_per_step": round(us / 1e3, 4),
+            "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int8",
+            "data": "synthetic (seed 20261201+0), resident in HBM",
+            "config": {"workload": "C1 single W8A8 linear", "m": m, "k": kk, "n": n},
+            "gpu_matches_cpu_torch_path": exact,
+            "cpu_baseline": {"value": round(ops / cpu_s / 1e12, 4), "unit": "TOPS", "cores": threads,
+                             "kind": "port", "ms": round(cpu_s * 1e3, 1),
+                             "sample": "the whole config: torch CPU quantize, torch._int_mm, epilogue "
+                                       "(median of 3)"}}
+
+
+def run_c5(args):
+    """Benchmark config 5: the projection chain at T = 12288 video + 317 text
+    tokens (M not a tile multiple) with six per-frame modulation rows
+    (indices = min(t // 2048, 5) for video tokens, 0 for text), and the
+    decode-like M = 256 projections (K = 5120, N = 5120 and 20480), whose
+    roofline is HBM on the int8 weights."""
+    import torch
+    from lynnreal_omni_amd import kernels as k
+    from lynnreal_omni_amd.int8_gemm import int8_matmul
+
+    video, text = 12288, 317
+    tokens = video + text
+    data = make_inputs(tokens, args.hidden, args.ffn, 20261201 + 4)
+    g = torch.Generator().manual_seed(20261201 + 4)
+    data.table = (0.1 * torch.randn(6, 6 * args.hidden, generator=g)).bfloat16()
+    data.indices = torch.cat([torch.clamp(torch.arange(video) // 2048, max=5),
+                              torch.zeros(text, dtype=torch.int64)])
+    sub = types.SimpleNamespace(**vars(args))
+    sub.tokens, sub.vendor_gemm = tokens, False
+    _, step_ms, kern_us, _ = run_gpu(sub, data)
+    ops = gemm_ops(tokens, args.hidden, args.ffn)
+    ms = statistics.mean(step_ms)
+    skinny = {}
+    for n in (5120, 20480):
+        kk = 5120
+        a = torch.randint(-127, 128, (256, kk), dtype=torch.int8, generator=g).cuda()
+        w = torch.randint(-127, 128, (n, kk), dtype=torch.int8, generator=g).cuda()
+        rs = (torch.rand(256, generator=g) / 127).cuda()
+        cs = (torch.rand(n, generator=g) * 4e-3 + 1e-3).cuda()
+        us = _event_time(lambda: int8_matmul(a, w.t(), rs, cs), 50)
+        nbytes = n * kk + 256 * kk + 2 * 256 * n
+        skinny[f"m256_n{n}"] = {"us": round(us, 2), "GB/s": round(nbytes / (us * 1e-6) / 1e9, 1),
+                                "hbm_frac": round(nbytes / (us * 1e-6) / 1e9 / PEAK_HBM_GBS, 4),
+                                "tops": round(2 * 256 * n * kk / (us * 1e-6) / 1e12, 1)}
+    return {"metric": "C5 ragged chain TOPS (T=12605, per-frame modulation) + M=256 projections",
+            "value": round(sum(ops.values()) / (ms * 1e-3) / 1e12, 2), "unit": "TOPS", "n_gpus": 1,
+            "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4),
+            "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int8",
+            "data": "synthetic (seed 20261201+4), resident in HBM",
+            "config": {"workload": "C5 ragged chain", "tokens": tokens, "table_rows": 6,
+                       "hidden": args.hidden, "ffn": args.ffn},
+            "kernels_us": {n: round(v, 2) for n, v in kern_us.items()}, "m256": skinny}
+
+
 def run_c4(args):
     """Benchmark config 4: W8A8 FFN at T=65536 against the same shapes in bf16.
 
@@ -382,6 +493,14 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py needs a GPU", file=sys.stderr)
         return 1
+    if args.workload == "c1":
+        log(f"device {torch.cuda.get_device_name(0)}; C1 W8A8 linear")
+        print(json.dumps(run_c1(args)), flush=True)
+        return 0
+    if args.workload == "c5":
+        log(f"device {torch.cuda.get_device_name(0)}; C5 ragged chain and M=256 projections")
+        print(json.dumps(run_c5(args)), flush=True)
+        return 0
     if args.workload == "c4":
         if args.tokens == 12288:
             args.tokens = 65536

@@ -35,6 +35,11 @@
 // Raise the wave's priority for the MFMA stream of each k-step (the two
 // waves of a SIMD then issue their MFMAs back to back instead of trading
 // issue slots with the other wave's memory instructions): +2% on QKV.
+// Ring depth of the 64x128 tile (both operands): its k-steps are small, so
+// more of them fit in LDS in flight.
+#ifndef GEMM_DEPTH_SMALL
+#define GEMM_DEPTH_SMALL 4
+#endif
 #ifndef GEMM_SETPRIO
 #define GEMM_SETPRIO 1
 #endif
@@ -308,7 +313,7 @@ __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t rsrc, void* lds, ui
 // +4 for the second k64 half) each group of 8 lanes then reads 8 distinct
 // 16-byte bank groups; measured on gfx950 this runs ds_read_b128 at 94% of
 // the rate of a contiguous read (an extra (R / 8) % 2 term drops it to 71%).
-template <int BM, int BN, int WAVES_M, int WAVES_N, int EPI, bool BIAS>
+template <int BM, int BN, int WAVES_M, int WAVES_N, int EPI, bool BIAS, int NA, int NB>
 __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_fast(GemmArgs p) {
   constexpr int BK = 128;
   constexpr int NWAVES = WAVES_M * WAVES_N;
@@ -317,8 +322,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_fast(GemmArgs p) 
   constexpr int A_BYTES = BM * BK, B_BYTES = BN * BK;
   constexpr int A_LOADS = BM / 8 / NWAVES, B_LOADS = BN / 8 / NWAVES;  // 1 KB DMAs per wave per k-step
   // A k-steps live in a ring of NA LDS slots, W k-steps in a ring of NB: an
-  // operand with 3 slots is fetched two k-steps ahead, with 2 one k-step.
-  constexpr int NA = GEMM_RING_A, NB = GEMM_RING_B;
+  // operand with d slots is fetched d - 1 k-steps ahead.
   static_assert(NWAVES == 4 || NWAVES == 8, "4 or 8 waves");
   static_assert(A_LOADS * NWAVES * 8 == BM && B_LOADS * NWAVES * 8 == BN && A_LOADS >= 1 &&
                     B_LOADS >= 1 && FM >= 1 && FN >= 1, "tile shape");
@@ -404,15 +408,29 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_fast(GemmArgs p) 
   // shallower ring's next k-step is issued first, then the deeper ring's.
   // Each wave's DMAs complete in issue order, so when k-step kt starts only
   // the deeper ring's newest k-step may still be in flight.
-  static_assert((NA == 2 || NA == 3) && (NB == 2 || NB == 3), "ring depths");
-  constexpr int kLater = NA > NB ? A_LOADS : (NB > NA ? B_LOADS : 0);
+  // Every k-step issues the shallower ring's next k-step first (first half)
+  // and the deeper ring's second (both rings in that order when equal), and
+  // the prologue issues its k-steps in the same interleaved order. At the
+  // barrier of k-step kt, the DMAs still allowed in flight are those issued
+  // after both A(kt) and B(kt):
+  //   B first: min((NA - 2)(A + B), (NB - 2)(A + B) + A) loads per wave,
+  //   A first: min((NB - 2)(A + B), (NA - 2)(A + B) + B).
+  static_assert(NA >= 2 && NB >= 2, "ring depths");
+  constexpr bool kBFirst = NB <= NA;
+  constexpr int kStep = A_LOADS + B_LOADS;
+  constexpr int kAfterA = kBFirst ? (NA - 2) * kStep : (NA - 2) * kStep + B_LOADS;
+  constexpr int kAfterB = kBFirst ? (NB - 2) * kStep + A_LOADS : (NB - 2) * kStep;
+  constexpr int kLater = kAfterA < kAfterB ? kAfterA : kAfterB;
+  static_assert(kLater >= 0 && kLater <= 63, "vmcnt range");
   constexpr int kWait = 0x70 | 0xf00 | (kLater & 0xf) | ((kLater >> 4) << 14);  // vmcnt(kLater)
-  if (NB <= NA) {
-    for (int s = 0; s < NB - 1; ++s) issue_b(s);
-    for (int s = 0; s < NA - 1; ++s) issue_a(s);
-  } else {
-    for (int s = 0; s < NA - 1; ++s) issue_a(s);
-    for (int s = 0; s < NB - 1; ++s) issue_b(s);
+  for (int s = 0; s < (NA > NB ? NA : NB) - 1; ++s) {
+    if (kBFirst) {
+      if (s < NB - 1) issue_b(s);
+      if (s < NA - 1) issue_a(s);
+    } else {
+      if (s < NA - 1) issue_a(s);
+      if (s < NB - 1) issue_b(s);
+    }
   }
   // One k-step: the first half's fragments are read, then its FM*FN MFMAs run
   // with the second half's fragment reads and the shallower ring's DMAs
@@ -422,7 +440,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_fast(GemmArgs p) 
   // barriers pin that order.
   constexpr int NMF = FM * FN;
   constexpr int NR1 = FM + FN;
-  constexpr bool B_FIRST = NB <= NA;
+  constexpr bool B_FIRST = kBFirst;
   constexpr int L1 = B_FIRST ? B_LOADS : A_LOADS, L2 = B_FIRST ? A_LOADS : B_LOADS;
   for (int kt = 0; kt < KT; ++kt) {
     __builtin_amdgcn_s_waitcnt(kWait);
@@ -546,12 +564,13 @@ struct FastCfg {
   int bm, bn;
 };
 
-template <int BM, int BN, int WAVES_M, int WAVES_N, int EPI, bool BIAS>
+template <int BM, int BN, int WAVES_M, int WAVES_N, int EPI, bool BIAS, int NA = GEMM_RING_A,
+          int NB = GEMM_RING_B>
 void launch_fast_cfg(GemmArgs& p, hipStream_t st) {
   p.tiles_m = (int)((p.m + BM - 1) / BM);
   p.tiles_n = (int)((p.n + BN - 1) / BN);
   const unsigned grid = (unsigned)(p.tiles_m * p.tiles_n);
-  hipLaunchKernelGGL((gemm_fast<BM, BN, WAVES_M, WAVES_N, EPI, BIAS>), dim3(grid),
+  hipLaunchKernelGGL((gemm_fast<BM, BN, WAVES_M, WAVES_N, EPI, BIAS, NA, NB>), dim3(grid),
                      dim3(64 * WAVES_M * WAVES_N), 0, st, p);
 }
 
@@ -565,9 +584,12 @@ void launch_fast(int tile, GemmArgs& p, hipStream_t st) {
     // 4 waves of 128x64 / 64x128; two 48 KB k-steps.
     case LR_TILE_256x128: launch_fast_cfg<256, 128, 2, 2, EPI, BIAS>(p, st); break;
     case LR_TILE_128x256: launch_fast_cfg<128, 256, 2, 2, EPI, BIAS>(p, st); break;
-    // 4 waves of 64x64; two 32 KB k-steps: 2 blocks per CU.
+    // 4 waves of 64x64; 80 KB of rings: 2 blocks per CU.
     case LR_TILE_128x128: launch_fast_cfg<128, 128, 2, 2, EPI, BIAS>(p, st); break;
-    default: launch_fast_cfg<64, 128, 1, 4, EPI, BIAS>(p, st); break;
+    // 4 waves of 64x32 (24 KB k-steps), both operands GEMM_DEPTH_SMALL - 1
+    // k-steps ahead: small-M GEMMs are bound by the DMA latency of their few
+    // tiles, not by LDS or MFMA.
+    default: launch_fast_cfg<64, 128, 1, 4, EPI, BIAS, GEMM_DEPTH_SMALL, GEMM_DEPTH_SMALL>(p, st); break;
   }
 }
 
@@ -602,15 +624,21 @@ int tile_cols(int tile) {
   }
 }
 
-// Shape heuristic from measured sweeps on MI355X (256 CUs): the 8-wave
-// 256x256 tile (64x128 per wave) once there are two tiles per CU, 128x128
-// for medium grids, 64x128 for small M (decode-like, weight-bandwidth bound).
+// Shape heuristic from measured sweeps on MI355X (256 CUs, K = 5120, M from
+// 64 to 12288, N from 5120 to 20480). A launch takes as many waves of tiles
+// as its tile count fills the resident blocks (one 256x256 or 64x128 block
+// per CU, two 128x128 blocks), and a wave of K = 5120 tiles took about
+// 66 us (256x256), 36 us (128x128) and 18 us (64x128): the shape with the
+// fewest wave-microseconds wins, ties to the larger tile.
 int auto_tile(int64_t m, int64_t n) {
   const int64_t cus = 256;
   auto tiles = [&](int t) { return ((m + tile_rows(t) - 1) / tile_rows(t)) * ((n + tile_cols(t) - 1) / tile_cols(t)); };
-  if (tiles(LR_TILE_256x256_W4x2) >= 2 * cus) return LR_TILE_256x256_W4x2;
-  if (tiles(LR_TILE_128x128) >= 4 * cus) return LR_TILE_128x128;
-  return LR_TILE_64x128;
+  auto waves = [&](int t, int64_t slots) { return (tiles(t) + slots - 1) / slots; };
+  const int64_t c256 = waves(LR_TILE_256x256_W4x2, cus) * 66;
+  const int64_t c128 = waves(LR_TILE_128x128, 2 * cus) * 36;
+  const int64_t c64 = waves(LR_TILE_64x128, cus) * 18;
+  if (c256 <= c128 && c256 <= c64) return LR_TILE_256x256_W4x2;
+  return c128 <= c64 ? LR_TILE_128x128 : LR_TILE_64x128;
 }
 
 }  // namespace
