@@ -258,6 +258,51 @@ __device__ __forceinline__ void store_tile_staged(const GemmArgs& p, const v4i (
   constexpr int ITERS = WM * CPR / 64;   // rows of 16-byte chunks per lane
   static_assert(WM * CPR % 64 == 0, "staging tile shape");
   const bool seq_covers = p.sequence >= p.m;
+  if constexpr (EPI == EPI_GATED && WM <= 64 && ITERS % 4 == 0) {
+    // x + bf16(gate * y): the residual and gate chunks of 4 staging rows are
+    // loaded before any of them is used, from clamped (always valid)
+    // addresses, so the loads overlap instead of each waiting in turn (a load
+    // under a branch, or after a store the compiler cannot prove disjoint,
+    // would serialise them). The table row of each of the wave's WM rows is
+    // read once, by lane r, and fetched per chunk with ds_bpermute.
+    const int64_t my_row = m0 + wm * WM + (lane < WM ? lane : 0);
+    const int tr_lane = (int)clamp_index(
+        p.indices[my_row < p.m ? (seq_covers ? my_row : my_row % p.sequence) : 0], p.table_rows);
+    constexpr int BATCH = 4;
+#pragma unroll 1
+    for (int s0 = 0; s0 < ITERS; s0 += BATCH) {
+      uint4 xv[BATCH], gv[BATCH], v[BATCH];
+      int64_t o[BATCH];
+      bool ok[BATCH];
+#pragma unroll
+      for (int b = 0; b < BATCH; ++b) {
+        const int q = (s0 + b) * 64 + lane;
+        const int r = q / CPR, ch = q % CPR;
+        const int64_t row = m0 + wm * WM + r;
+        const int64_t col = n0 + wn * WN + ch * 8;
+        ok[b] = row < p.m && col < p.n;
+        const int64_t row_l = ok[b] ? row : m0, col_l = ok[b] ? col : n0;
+        o[b] = row * p.n + col;
+        const int tr = __builtin_amdgcn_ds_bpermute(4 * r, tr_lane);
+        xv[b] = *reinterpret_cast<const uint4*>(p.resid + row_l * p.n + col_l);
+        gv[b] = *reinterpret_cast<const uint4*>(p.table + (int64_t)tr * p.table_width +
+                                                 (int64_t)p.gate_slot * p.n + col_l);
+        v[b] = *reinterpret_cast<const uint4*>(stage + r * PITCH + ch * 16);
+      }
+#pragma unroll
+      for (int b = 0; b < BATCH; ++b) {
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          const uint32_t u = word_of(v[b], w), x = word_of(xv[b], w), g = word_of(gv[b], w);
+          const uint32_t y = pack_bf2(bf_lo(x) + round_bf(bf_lo(g) * bf_lo(u)),
+                                      bf_hi(x) + round_bf(bf_hi(g) * bf_hi(u)));
+          if (w == 0) v[b].x = y; else if (w == 1) v[b].y = y; else if (w == 2) v[b].z = y; else v[b].w = y;
+        }
+        if (ok[b]) *reinterpret_cast<uint4*>(static_cast<uint16_t*>(p.c) + o[b]) = v[b];
+      }
+    }
+    return;
+  }
 #pragma unroll 4
   for (int s = 0; s < ITERS; ++s) {
     const int q = s * 64 + lane;
