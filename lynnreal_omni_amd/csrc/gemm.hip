@@ -202,6 +202,13 @@ __device__ __forceinline__ void store_tile(const GemmArgs& p, const v4i (&acc)[F
   }
 }
 
+// Whole-line output stores, non-temporal: the output is not read again by
+// this kernel, and streaming it keeps the L2 for the operand panels (FFN-up
+// 1135 -> 1107 us, the other projections 1-2% faster).
+__device__ __forceinline__ void store_c16(uint16_t* dst, const uint4& v) {
+  store_nt(reinterpret_cast<uint4*>(dst), v);
+}
+
 __device__ __forceinline__ uint32_t word_of(const uint4& v, int i) {
   return i == 0 ? v.x : (i == 1 ? v.y : (i == 2 ? v.z : v.w));
 }
@@ -298,7 +305,7 @@ __device__ __forceinline__ void store_tile_staged(const GemmArgs& p, const v4i (
                                       bf_hi(x) + round_bf(bf_hi(g) * bf_hi(u)));
           if (w == 0) v[b].x = y; else if (w == 1) v[b].y = y; else if (w == 2) v[b].z = y; else v[b].w = y;
         }
-        if (ok[b]) *reinterpret_cast<uint4*>(static_cast<uint16_t*>(p.c) + o[b]) = v[b];
+        if (ok[b]) store_c16(static_cast<uint16_t*>(p.c) + o[b], v[b]);
       }
     }
     return;
@@ -332,7 +339,7 @@ __device__ __forceinline__ void store_tile_staged(const GemmArgs& p, const v4i (
           if (w == 0) v.x = y; else if (w == 1) v.y = y; else if (w == 2) v.z = y; else v.w = y;
         }
       }
-      *reinterpret_cast<uint4*>(static_cast<uint16_t*>(p.c) + o) = v;
+      store_c16(static_cast<uint16_t*>(p.c) + o, v);
     }
   }
 }

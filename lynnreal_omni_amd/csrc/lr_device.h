@@ -50,15 +50,23 @@ __device__ __forceinline__ uint4 buf_load16_reused(__amdgpu_buffer_rsrc_t r, uin
   const v4u v = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
   return make_uint4(v.x, v.y, v.z, v.w);
 }
+// Cache policies of the row stores (measured on MI355X at 12288 rows of
+// 5120): 8-byte stores (int8 rows) go out non-temporal (nt), which took the
+// fused norm + quant from 42 to 38 us and the 5120-wide quantizer from 31 to
+// 29 us; 16-byte stores (bf16 rows) write through to system scope (sc0 sc1),
+// 4% faster for the bf16 norm, where nt made it 10% slower. Either way no
+// dirty output lines are left in L2 for the end-of-kernel write-back.
+constexpr int kStore16Policy = 0x11;  // sc0 | sc1
+constexpr int kStore8Policy = 0x2;    // nt
 __device__ __forceinline__ void buf_store16(__amdgpu_buffer_rsrc_t r, uint32_t voff,
                                             uint32_t soff, uint4 v) {
   const v4u w = {v.x, v.y, v.z, v.w};
-  __builtin_amdgcn_raw_buffer_store_b128(w, r, voff, soff, 0);
+  __builtin_amdgcn_raw_buffer_store_b128(w, r, voff, soff, kStore16Policy);
 }
 __device__ __forceinline__ void buf_store8(__amdgpu_buffer_rsrc_t r, uint32_t voff,
                                            uint32_t soff, uint2 v) {
   const v2u w = {v.x, v.y};
-  __builtin_amdgcn_raw_buffer_store_b64(w, r, voff, soff, 0);
+  __builtin_amdgcn_raw_buffer_store_b64(w, r, voff, soff, kStore8Policy);
 }
 
 // ---------------------------------------------------------------- bf16 ----
