@@ -156,7 +156,8 @@ __device__ __forceinline__ void store_tile(const GemmArgs& p, const v4i (&acc)[F
 #pragma unroll
         for (int i = 0; i < FM; ++i)
           if (rows[i] < p.m)
-            *reinterpret_cast<v4i*>(static_cast<int32_t*>(p.c) + rows[i] * p.n + col) = acc[i][j];
+            store_nt(reinterpret_cast<uint4*>(static_cast<int32_t*>(p.c) + rows[i] * p.n + col),
+                     make_uint4(acc[i][j][0], acc[i][j][1], acc[i][j][2], acc[i][j][3]));
         continue;
       }
       const float4 cs = *reinterpret_cast<const float4*>(p.cs + col);

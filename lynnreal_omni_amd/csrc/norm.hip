@@ -347,11 +347,16 @@ __global__ __launch_bounds__((64 * stream_waves<CPL, RESID>())) void rms_adaln_s
       lds[(2 * a + 1) * cap + c] = make_float4(f[4], f[5], f[6], f[7]);
     }
   }
-  // Does every row of the slice use the staged table row?
+  // Does every row of the slice use the staged table row? (Always, with a
+  // one-row table: then the index reads and their latency are skipped.)
   int same = 1;
-  for (int64_t r = start + threadIdx.x; r < end; r += kStreamThreads)
-    same &= clamp_index(p.indices[r % p.sequence], p.table_rows) == tr_lds;
-  same = __syncthreads_and(same);
+  if (p.table_rows > 1) {
+    for (int64_t r = start + threadIdx.x; r < end; r += kStreamThreads)
+      same &= clamp_index(p.indices[r % p.sequence], p.table_rows) == tr_lds;
+    same = __syncthreads_and(same);
+  } else {
+    __syncthreads();
+  }
 
   const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   int64_t row = start + wave;
