@@ -272,7 +272,8 @@ __device__ __forceinline__ void store_tile_staged(const GemmArgs& p, const v4i (
     // addresses, so the loads overlap instead of each waiting in turn (a load
     // under a branch, or after a store the compiler cannot prove disjoint,
     // would serialise them). The table row of each of the wave's WM rows is
-    // read once, by lane r, and fetched per chunk with ds_bpermute.
+    // read once, by lane r, and fetched per chunk with ds_bpermute. The
+    // residual is read once (non-temporal loads); the gate rows are shared.
     const int64_t my_row = m0 + wm * WM + (lane < WM ? lane : 0);
     const int tr_lane = (int)clamp_index(
         p.indices[my_row < p.m ? (seq_covers ? my_row : my_row % p.sequence) : 0], p.table_rows);
@@ -292,7 +293,7 @@ __device__ __forceinline__ void store_tile_staged(const GemmArgs& p, const v4i (
         const int64_t row_l = ok[b] ? row : m0, col_l = ok[b] ? col : n0;
         o[b] = row * p.n + col;
         const int tr = __builtin_amdgcn_ds_bpermute(4 * r, tr_lane);
-        xv[b] = *reinterpret_cast<const uint4*>(p.resid + row_l * p.n + col_l);
+        xv[b] = load_nt(reinterpret_cast<const uint4*>(p.resid + row_l * p.n + col_l));
         gv[b] = *reinterpret_cast<const uint4*>(p.table + (int64_t)tr * p.table_width +
                                                  (int64_t)p.gate_slot * p.n + col_l);
         v[b] = *reinterpret_cast<const uint4*>(stage + r * PITCH + ch * 16);
@@ -329,7 +330,7 @@ __device__ __forceinline__ void store_tile_staged(const GemmArgs& p, const v4i (
         }
       } else if (EPI == EPI_GATED) {
         const int64_t tr = clamp_index(p.indices[seq_covers ? row : row % p.sequence], p.table_rows);
-        const uint4 xv = *reinterpret_cast<const uint4*>(p.resid + o);
+        const uint4 xv = load_nt(reinterpret_cast<const uint4*>(p.resid + o));
         const uint4 gv = *reinterpret_cast<const uint4*>(
             p.table + tr * p.table_width + (int64_t)p.gate_slot * p.n + col);
 #pragma unroll
