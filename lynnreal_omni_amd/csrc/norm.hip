@@ -170,7 +170,11 @@ __global__ __launch_bounds__(kThreads) void rms_adaln_kernel(NormArgs p) {
 // fp32: gamma, bf16(1 + scale), shift and (residual) gate. Wave w of W then
 // streams rows start + w, start + w + W, ... and reads the parameters from
 // LDS (their waits, lgkmcnt, do not wait for row loads in flight). A slice
-// whose rows use several table rows reads its parameters from global memory.
+// that spans two runs of equal table rows (a frame boundary of per-frame
+// modulation) processes the first run, restages the second run's row and
+// processes the rest; a slice with more runs reads its parameters from
+// global memory. Slices are ceil(rows / resident blocks) rows, so every CU
+// gets the same share whatever the frame length.
 // Waves per block: 16 (four per SIMD, one row per wave at a time) for rows up
 // to 5120 wide without a residual, else 8 (two rows per wave, the next one's
 // loads in flight). The LDS block is per block, so more waves per block share it.
@@ -388,18 +392,13 @@ __device__ __forceinline__ void norm_row_f32(const NormArgs& p, int64_t row, con
   }
 }
 
-template <int CPL, bool RESID, bool QUANT>
-__global__ __launch_bounds__((64 * stream_waves<CPL, RESID>())) void rms_adaln_stream(
-    NormArgs p, int64_t rows, int64_t per_block) {
-  constexpr int kStreamWaves = stream_waves<CPL, RESID>();
-  constexpr int kStreamThreads = 64 * kStreamWaves;
+// Expands the parameters of table row tr into LDS (every thread of the block
+// takes part).
+template <int CPL, bool RESID, int THREADS>
+__device__ __forceinline__ void stage_params(const NormArgs& p, float4* lds, int64_t tr) {
   constexpr int cap = 64 * CPL;
-  __shared__ float4 lds[(RESID ? 8 : 6) * cap];
-  const int64_t start = (int64_t)blockIdx.x * per_block;
-  const int64_t end = start + per_block < rows ? start + per_block : rows;
-  const int64_t tr_lds = clamp_index(p.indices[start % p.sequence], p.table_rows);
-  const uint16_t* trow = p.table + tr_lds * p.table_width;
-  for (int c = threadIdx.x; c < cap; c += kStreamThreads) {
+  const uint16_t* trow = p.table + tr * p.table_width;
+  for (int c = threadIdx.x; c < cap; c += THREADS) {
     const int na = RESID ? 4 : 3;
     for (int a = 0; a < na; ++a) {
       float f[8];
@@ -408,51 +407,92 @@ __global__ __launch_bounds__((64 * stream_waves<CPL, RESID>())) void rms_adaln_s
       lds[(2 * a + 1) * cap + c] = make_float4(f[4], f[5], f[6], f[7]);
     }
   }
-  // Does every row of the slice use the staged table row? (Always, with a
-  // one-row table: then the index reads and their latency are skipped.)
-  int same = 1;
-  if (p.table_rows > 1) {
-    for (int64_t r = start + threadIdx.x; r < end; r += kStreamThreads)
-      same &= clamp_index(p.indices[r % p.sequence], p.table_rows) == tr_lds;
-    same = __syncthreads_and(same);
-  } else {
-    __syncthreads();
-  }
+}
 
-  const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
-  int64_t row = start + wave;
-  if (!same) {
-    // Mixed table rows: parameters from global memory, one row at a time.
-    RowRegs<CPL, RESID> rg;
-    for (; row < end; row += kStreamWaves) {
-      load_row(p, row, rg);
-      const int64_t tr = clamp_index(p.indices[row % p.sequence], p.table_rows);
-      norm_row<CPL, RESID, QUANT, false>(p, row, p.table + tr * p.table_width, nullptr, rg);
-    }
-    return;
-  }
+// Rows [lo, hi) of the block's slice with the parameters staged in LDS; wave
+// w takes rows lo + w, lo + w + WAVES, ...
+template <int CPL, bool RESID, bool QUANT, int WAVES>
+__device__ __forceinline__ void run_rows(const NormArgs& p, const float4* lds, int64_t lo,
+                                         int64_t hi, int wave) {
+  int64_t row = lo + wave;
   if constexpr (single_buffer<CPL, RESID>()) {
     RowRegs<CPL, RESID> r1;
-    for (; row < end; row += kStreamWaves) {
+    for (; row < hi; row += WAVES) {
       load_row(p, row, r1);
       norm_row_f32<CPL, QUANT>(p, row, lds, r1);
     }
+  } else {
+    RowRegs<CPL, RESID> ra, rb;
+    if (row >= hi) return;
+    load_row(p, row, ra);
+    while (true) {
+      const int64_t next = row + WAVES;
+      load_row(p, next, rb, next < hi);  // zeros past the range, no memory access
+      norm_row<CPL, RESID, QUANT, true>(p, row, nullptr, lds, ra);
+      row = next;
+      if (row >= hi) break;
+      const int64_t after = row + WAVES;
+      load_row(p, after, ra, after < hi);
+      norm_row<CPL, RESID, QUANT, true>(p, row, nullptr, lds, rb);
+      row = after;
+      if (row >= hi) break;
+    }
+  }
+}
+
+template <int CPL, bool RESID, bool QUANT>
+__global__ __launch_bounds__((64 * stream_waves<CPL, RESID>())) void rms_adaln_stream(
+    NormArgs p, int64_t rows, int64_t per_block) {
+  constexpr int kStreamWaves = stream_waves<CPL, RESID>();
+  constexpr int kStreamThreads = 64 * kStreamWaves;
+  constexpr int cap = 64 * CPL;
+  __shared__ float4 lds[(RESID ? 8 : 6) * cap];
+  __shared__ int first_other;
+  const int64_t start = (int64_t)blockIdx.x * per_block;
+  const int64_t end = start + per_block < rows ? start + per_block : rows;
+  const int wave = __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const int64_t tr_first = clamp_index(p.indices[start % p.sequence], p.table_rows);
+  stage_params<CPL, RESID, kStreamThreads>(p, lds, tr_first);
+  if (p.table_rows == 1) {
+    // One table row: every row of the slice uses the staged parameters.
+    __syncthreads();
+    run_rows<CPL, RESID, QUANT, kStreamWaves>(p, lds, start, end, wave);
     return;
   }
-  RowRegs<CPL, RESID> ra, rb;
-  if (row >= end) return;
-  load_row(p, row, ra);
-  while (true) {
-    const int64_t next = row + kStreamWaves;
-    load_row(p, next, rb, next < end);  // zeros past the slice, no memory access
-    norm_row<CPL, RESID, QUANT, true>(p, row, nullptr, lds, ra);
-    row = next;
-    if (row >= end) break;
-    const int64_t after = row + kStreamWaves;
-    load_row(p, after, ra, after < end);
-    norm_row<CPL, RESID, QUANT, true>(p, row, nullptr, lds, rb);
-    row = after;
-    if (row >= end) break;
+  // The slice is one run of equal table rows, two runs (a frame boundary of
+  // per-frame modulation), or mixed. split = the first row of the second run.
+  if (threadIdx.x == 0) first_other = (int)(end - start);
+  __syncthreads();
+  for (int64_t r = start + threadIdx.x; r < end; r += kStreamThreads) {
+    if (clamp_index(p.indices[r % p.sequence], p.table_rows) != tr_first) {
+      atomicMin(&first_other, (int)(r - start));
+      break;
+    }
+  }
+  __syncthreads();
+  const int64_t split = start + __builtin_amdgcn_readfirstlane(first_other);
+  if (split == end) {
+    run_rows<CPL, RESID, QUANT, kStreamWaves>(p, lds, start, end, wave);
+    return;
+  }
+  const int64_t tr_second = clamp_index(p.indices[split % p.sequence], p.table_rows);
+  int second_run = 1;
+  for (int64_t r = split + threadIdx.x; r < end; r += kStreamThreads)
+    second_run &= clamp_index(p.indices[r % p.sequence], p.table_rows) == tr_second;
+  if (__syncthreads_and(second_run)) {
+    run_rows<CPL, RESID, QUANT, kStreamWaves>(p, lds, start, split, wave);
+    __syncthreads();  // every wave is done with the first run's parameters
+    stage_params<CPL, RESID, kStreamThreads>(p, lds, tr_second);
+    __syncthreads();
+    run_rows<CPL, RESID, QUANT, kStreamWaves>(p, lds, split, end, wave);
+    return;
+  }
+  // Mixed table rows: parameters from global memory, one row at a time.
+  RowRegs<CPL, RESID> rg;
+  for (int64_t row = start + wave; row < end; row += kStreamWaves) {
+    load_row(p, row, rg);
+    const int64_t tr = clamp_index(p.indices[row % p.sequence], p.table_rows);
+    norm_row<CPL, RESID, QUANT, false>(p, row, p.table + tr * p.table_width, nullptr, rg);
   }
 }
 
@@ -472,8 +512,7 @@ void launch_stream(const NormArgs& p, int64_t rows, hipStream_t st) {
     resident = nb;
   }
   const int64_t slots = (int64_t)compute_units() * resident;
-  int64_t per_block = (rows + slots - 1) / slots;
-  per_block = (per_block + kStreamWaves - 1) / kStreamWaves * kStreamWaves;
+  const int64_t per_block = (rows + slots - 1) / slots;
   const int64_t grid = (rows + per_block - 1) / per_block;
   hipLaunchKernelGGL(kernel, dim3((unsigned)grid), dim3(kStreamThreads), 0, st, p, rows,
                      per_block);
