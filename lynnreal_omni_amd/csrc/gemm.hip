@@ -635,6 +635,9 @@ void launch_fast(int tile, GemmArgs& p, hipStream_t st) {
     case LR_TILE_256x256: launch_fast_cfg<256, 256, 2, 4, EPI, BIAS>(p, st); break;
     // 8 waves of 64x128 (same block shape, other wave grid).
     case LR_TILE_256x256_W4x2: launch_fast_cfg<256, 256, 4, 2, EPI, BIAS>(p, st); break;
+    // 8 waves of 64x96: 192-column tiles fill the CUs where 256-column ones leave a
+    // partial wave (N = 5120 at M = 2048: 216 tiles instead of 160).
+    case LR_TILE_256x192: launch_fast_cfg<256, 192, 4, 2, EPI, BIAS>(p, st); break;
     // 4 waves of 128x64 / 64x128; two 48 KB k-steps.
     case LR_TILE_256x128: launch_fast_cfg<256, 128, 2, 2, EPI, BIAS>(p, st); break;
     case LR_TILE_128x256: launch_fast_cfg<128, 256, 2, 2, EPI, BIAS>(p, st); break;
@@ -666,7 +669,8 @@ void dispatch_bias(bool generic, int tile, bool bias, GemmArgs& p, hipStream_t s
 
 int tile_rows(int tile) {
   switch (tile) {
-    case LR_TILE_256x256: case LR_TILE_256x256_W4x2: case LR_TILE_256x128: return 256;
+    case LR_TILE_256x256: case LR_TILE_256x256_W4x2: case LR_TILE_256x128: case LR_TILE_256x192:
+      return 256;
     case LR_TILE_128x256: case LR_TILE_128x128: return 128;
     default: return 64;
   }
@@ -674,23 +678,28 @@ int tile_rows(int tile) {
 int tile_cols(int tile) {
   switch (tile) {
     case LR_TILE_256x256: case LR_TILE_256x256_W4x2: case LR_TILE_128x256: return 256;
+    case LR_TILE_256x192: return 192;
     default: return 128;
   }
 }
 
 // Shape heuristic from measured sweeps on MI355X (256 CUs, K = 5120, M from
 // 64 to 12288, N from 5120 to 20480). A launch takes as many waves of tiles
-// as its tile count fills the resident blocks (one 256x256 or 64x128 block
-// per CU, two 128x128 blocks), and a wave of K = 5120 tiles took about
-// 66 us (256x256), 36 us (128x128) and 18 us (64x128): the shape with the
-// fewest wave-microseconds wins, ties to the larger tile.
+// as its tile count fills the resident blocks (one 256x256, 256x192 or 64x128
+// block per CU, two 128x128 blocks), and a wave of K = 5120 tiles took about
+// 66 us (256x256), 60 us (256x192), 36 us (128x128) and 18 us (64x128): the
+// shape with the fewest wave-microseconds wins, ties to the larger tile
+// (256x192 only when strictly better: M = 2048, N = 5120 runs 216 of its
+// tiles in one wave, 60 us against 67 us for 160 tiles of 256x256).
 int auto_tile(int64_t m, int64_t n) {
   const int64_t cus = 256;
   auto tiles = [&](int t) { return ((m + tile_rows(t) - 1) / tile_rows(t)) * ((n + tile_cols(t) - 1) / tile_cols(t)); };
   auto waves = [&](int t, int64_t slots) { return (tiles(t) + slots - 1) / slots; };
   const int64_t c256 = waves(LR_TILE_256x256_W4x2, cus) * 66;
+  const int64_t c192 = waves(LR_TILE_256x192, cus) * 60;
   const int64_t c128 = waves(LR_TILE_128x128, 2 * cus) * 36;
   const int64_t c64 = waves(LR_TILE_64x128, cus) * 18;
+  if (c192 < c256 && c192 < c128 && c192 < c64) return LR_TILE_256x192;
   if (c256 <= c128 && c256 <= c64) return LR_TILE_256x256_W4x2;
   return c128 <= c64 ? LR_TILE_128x128 : LR_TILE_64x128;
 }
@@ -711,7 +720,7 @@ extern "C" int lr_int8_gemm(const int8_t* a, const int8_t* b, int64_t b_stride_k
   LR_REQUIRE(m >= 0 && n >= 0 && k >= 0, "int8_gemm: negative shape");
   LR_REQUIRE(epilogue >= LR_EPI_BF16 && epilogue <= LR_EPI_RAW_INT32,
              "int8_gemm: unknown epilogue %d", epilogue);
-  LR_REQUIRE(tile >= LR_TILE_AUTO && tile <= LR_TILE_256x256_W4x2, "int8_gemm: unknown tile %d",
+  LR_REQUIRE(tile >= LR_TILE_AUTO && tile <= LR_TILE_256x192, "int8_gemm: unknown tile %d",
              tile);
   if (m == 0 || n == 0) return LR_OK;
   LR_REQUIRE(a && b && c, "int8_gemm: null A/B/C");

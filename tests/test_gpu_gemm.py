@@ -19,7 +19,8 @@ from oracle import reference as ref
 
 pytestmark = pytest.mark.gpu
 
-TILES = [None, (256, 256), "256x256_w4x2", (256, 128), (128, 256), (128, 128), (64, 128), "generic"]
+TILES = [None, (256, 256), "256x256_w4x2", (256, 192), (256, 128), (128, 256), (128, 128), (64, 128),
+         "generic"]
 
 
 def gen(seed):

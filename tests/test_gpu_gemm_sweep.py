@@ -14,11 +14,12 @@ from oracle import reference as ref
 
 pytestmark = pytest.mark.gpu
 
-TILES = [None, (256, 256), "256x256_w4x2", (256, 128), (128, 256), (128, 128), (64, 128), "generic"]
+TILES = [None, (256, 256), "256x256_w4x2", (256, 192), (256, 128), (128, 256), (128, 128), (64, 128),
+         "generic"]
 EPILOGUES = ["int32", "bf16", "gelu_tanh", "gated"]
 
 
-def _cases(count=32, seed=20261202):
+def _cases(count=36, seed=20261202):
     rng = np.random.default_rng(seed)
     out = []
     for i in range(count):
@@ -27,7 +28,7 @@ def _cases(count=32, seed=20261202):
         if i % 4 == 3:
             n += 4                                  # ... and N % 8 == 4 takes the direct stores
         k = int(rng.integers(1, 80)) * 16
-        # every tile meets every epilogue once over the 32 cases
+        # every tile meets every epilogue once over the 36 cases
         out.append((m, n, k, TILES[i % len(TILES)], EPILOGUES[(i + i // len(TILES)) % len(EPILOGUES)],
                     i % 3 != 0))
     return out

@@ -28,6 +28,7 @@ def test_tile_mapping():
     assert int8_gemm._tile_id((128, 256, 128, 8, 4, 8)) == 3
     assert int8_gemm._tile_id((64, 128, 128, 4, 3, 0)) == 5
     assert int8_gemm._tile_id("generic") == 6
+    assert int8_gemm._tile_id((256, 192, 128, 8, 3)) == 8
     for bad in ((32, 32, 64, 4, 2), (512, 512, 1, 1, 1), "fast", (1,)):
         with pytest.raises(ValueError):
             int8_gemm._tile_id(bad)
