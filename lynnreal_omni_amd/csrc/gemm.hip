@@ -346,6 +346,48 @@ __device__ __forceinline__ void store_tile_staged(const GemmArgs& p, const v4i (
   }
 }
 
+// The raw int32 accumulators through the same per-wave LDS staging area, in
+// two column halves (a whole int32 sub-tile is twice the bf16 one; each half
+// has the bf16 tile's size and row pitch): every store instruction writes
+// whole 128-byte lines. From the MFMA layout each row got 64-byte pieces,
+// about 14% more HBM writes than the output. Needs N % 4 == 0 and 16-byte
+// aligned C.
+template <int FM, int FN, int WM, int WN>
+__device__ __forceinline__ void store_tile_staged_raw(const GemmArgs& p, const v4i (&acc)[FM][FN],
+                                                      char* stage, int64_t m0, int64_t n0, int wm,
+                                                      int wn, int lane) {
+  static_assert(FN % 2 == 0, "two column halves");
+  constexpr int HALF = FN / 2, HW = WN / 2;
+  constexpr int PITCH = 4 * HW + 16;
+  constexpr int CPR = HW / 4;            // 16-byte chunks per staging row
+  constexpr int ITERS = WM * CPR / 64;
+  static_assert(WM * CPR % 64 == 0, "staging tile shape");
+  const int lr_ = lane & 15, lg = lane >> 4;
+  int32_t* const c = static_cast<int32_t*>(p.c);
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+#pragma unroll
+    for (int jj = 0; jj < HALF; ++jj)
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+        *reinterpret_cast<v4i*>(stage + (16 * i + lr_) * PITCH + (16 * jj + 4 * lg) * 4) =
+            acc[i][h * HALF + jj];
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's staging writes are done
+    asm volatile("" ::: "memory");
+#pragma unroll 4
+    for (int s = 0; s < ITERS; ++s) {
+      const int q = s * 64 + lane;
+      const int r = q / CPR, ch = q % CPR;
+      const int64_t row = m0 + wm * WM + r;
+      const int64_t col = n0 + wn * WN + h * HW + ch * 4;
+      const uint4 v = *reinterpret_cast<const uint4*>(stage + r * PITCH + ch * 16);
+      if (row < p.m && col < p.n) store_nt(reinterpret_cast<uint4*>(c + row * p.n + col), v);
+    }
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // the reads are done before the next half is written
+    asm volatile("" ::: "memory");
+  }
+}
+
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
 
 // 16 bytes per lane from a buffer resource straight into LDS: lane l writes
@@ -567,6 +609,10 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_fast(GemmArgs p) 
     __syncthreads();
     store_tile_staged<FM, FN, WM, WN, EPI, BIAS>(p, acc, smem + wave * WM * (2 * WN + 16), m0, n0,
                                                  wm, wn, lane);
+  } else if (EPI == EPI_RAW && p.nvec) {
+    __syncthreads();
+    store_tile_staged_raw<FM, FN, WM, WN>(p, acc, smem + wave * WM * (2 * WN + 16), m0, n0, wm, wn,
+                                          lane);
   } else {
     store_tile<FM, FN, WM, WN, EPI, BIAS>(p, acc, m0, n0, wm, wn, lane);
   }
