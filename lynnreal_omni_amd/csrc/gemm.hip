@@ -397,6 +397,11 @@ typedef __attribute__((address_space(3))) void* lds_ptr_t;
 __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t rsrc, void* lds, uint32_t voffset) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_ptr_t)lds, 16, voffset, 0, 0, 0);
 }
+// The same with a wave-uniform byte offset added (an SGPR operand).
+__device__ __forceinline__ void dma16s(__amdgpu_buffer_rsrc_t rsrc, void* lds, uint32_t voffset,
+                                       uint32_t soffset) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_ptr_t)lds, 16, voffset, soffset, 0, 0);
+}
 
 // ----------------------------------------------------------- fast GEMM ----
 // K is consumed in k-steps of 128 bytes; two k-steps live in LDS (double
@@ -409,7 +414,7 @@ __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t rsrc, void* lds, ui
 // +4 for the second k64 half) each group of 8 lanes then reads 8 distinct
 // 16-byte bank groups; measured on gfx950 this runs ds_read_b128 at 94% of
 // the rate of a contiguous read (an extra (R / 8) % 2 term drops it to 71%).
-template <int BM, int BN, int WAVES_M, int WAVES_N, int EPI, bool BIAS, int NA, int NB>
+template <int BM, int BN, int WAVES_M, int WAVES_N, int EPI, bool BIAS, int NA, int NB, bool KALIGNED>
 __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_fast(GemmArgs p) {
   constexpr int BK = 128;
   constexpr int NWAVES = WAVES_M * WAVES_N;
@@ -433,7 +438,8 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_fast(GemmArgs p) 
   int tm, tn;
   tile_coords(p, tm, tn);
   const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  // Wave-uniform, so that everything derived from it (LDS addresses, M0) stays scalar.
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int wm = wave / WAVES_N, wn = wave % WAVES_N;
   const int64_t K = p.k;
   const int KT = (int)((K + BK - 1) / BK);
@@ -455,33 +461,41 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_fast(GemmArgs p) 
 #pragma unroll
   for (int j = 0; j < B_LOADS; ++j) b_off[j] = (uint32_t)(((wave * B_LOADS + j) * 8 + drow) * K + dchunk);
 
-  // k-steps past the end (the rings keep issuing so that the wait counts stay
-  // fixed) read as zero without touching memory.
+  // With K % 128 == 0 a DMA's per-lane offset is fixed and the k-step goes in
+  // the scalar offset (no vector work per DMA). The rings keep issuing past the
+  // last k-step so that the wait counts stay fixed; those DMAs re-read the last
+  // k-step (every address stays inside the panel, whether or not the hardware
+  // bounds check counts the scalar offset) into slots no k-step reads again.
+  // With K % 128 != 0 the last k-step is partial: each lane picks an offset
+  // past the descriptor (zeros, no memory access) for chunks at or past K, and
+  // past the last k-step every lane does.
   auto dma_a = [&](int kt, int i) {
+    if constexpr (KALIGNED) {
+      dma16s(ra, a_ring + (kt % NA) * A_BYTES + (wave * A_LOADS + i) * 1024, a_off[i],
+             (uint32_t)((kt < KT ? kt : KT - 1) * BK));
+      return;
+    }
     const int64_t kbase = (int64_t)kt * BK;
     dma16(ra, a_ring + (kt % NA) * A_BYTES + (wave * A_LOADS + i) * 1024,
           kbase + dchunk < K ? a_off[i] + (uint32_t)kbase : 0x80000000u);
   };
   auto dma_b = [&](int kt, int j) {
+    if constexpr (KALIGNED) {
+      dma16s(rb, b_ring + (kt % NB) * B_BYTES + (wave * B_LOADS + j) * 1024, b_off[j],
+             (uint32_t)((kt < KT ? kt : KT - 1) * BK));
+      return;
+    }
     const int64_t kbase = (int64_t)kt * BK;
     dma16(rb, b_ring + (kt % NB) * B_BYTES + (wave * B_LOADS + j) * 1024,
           kbase + dchunk < K ? b_off[j] + (uint32_t)kbase : 0x80000000u);
   };
   auto issue_a = [&](int kt) {
-    const int64_t kbase = (int64_t)kt * BK;
-    char* dst = a_ring + (kt % NA) * A_BYTES;
 #pragma unroll
-    for (int i = 0; i < A_LOADS; ++i)
-      dma16(ra, dst + (wave * A_LOADS + i) * 1024,
-            kbase + dchunk < K ? a_off[i] + (uint32_t)kbase : 0x80000000u);
+    for (int i = 0; i < A_LOADS; ++i) dma_a(kt, i);
   };
   auto issue_b = [&](int kt) {
-    const int64_t kbase = (int64_t)kt * BK;
-    char* dst = b_ring + (kt % NB) * B_BYTES;
 #pragma unroll
-    for (int j = 0; j < B_LOADS; ++j)
-      dma16(rb, dst + (wave * B_LOADS + j) * 1024,
-            kbase + dchunk < K ? b_off[j] + (uint32_t)kbase : 0x80000000u);
+    for (int j = 0; j < B_LOADS; ++j) dma_b(kt, j);
   };
 
   // Fragment read: 16-row fragment f spans blocks 2f, 2f+1.
@@ -670,8 +684,12 @@ void launch_fast_cfg(GemmArgs& p, hipStream_t st) {
   p.tiles_m = (int)((p.m + BM - 1) / BM);
   p.tiles_n = (int)((p.n + BN - 1) / BN);
   const unsigned grid = (unsigned)(p.tiles_m * p.tiles_n);
-  hipLaunchKernelGGL((gemm_fast<BM, BN, WAVES_M, WAVES_N, EPI, BIAS, NA, NB>), dim3(grid),
-                     dim3(64 * WAVES_M * WAVES_N), 0, st, p);
+  if (p.k % 128 == 0)
+    hipLaunchKernelGGL((gemm_fast<BM, BN, WAVES_M, WAVES_N, EPI, BIAS, NA, NB, true>), dim3(grid),
+                       dim3(64 * WAVES_M * WAVES_N), 0, st, p);
+  else
+    hipLaunchKernelGGL((gemm_fast<BM, BN, WAVES_M, WAVES_N, EPI, BIAS, NA, NB, false>), dim3(grid),
+                       dim3(64 * WAVES_M * WAVES_N), 0, st, p);
 }
 
 template <int EPI, bool BIAS>
