@@ -1,7 +1,8 @@
 """A seeded sweep of the INT8 GEMM over odd shapes, every tile and every
 epilogue (model/int8_gemm.py:13-46; the epilogues of model/kernels.py:27-46,
 :131-153): M and N that are not tile multiples, K a multiple of 16 but not of
-the 128-byte k-step, with and without bias. int32, bf16 and gated-residual
+the 128-byte k-step (the per-lane DMA path) and K a multiple of it (the
+scalar-offset DMA path), with and without bias. int32, bf16 and gated-residual
 outputs are compared bit for bit with the oracle, GELU-tanh within the bf16
 tolerance. Each case is small; the point is the number of distinct tails."""
 import numpy as np
@@ -34,7 +35,19 @@ def _cases(count=36, seed=20261202):
     return out
 
 
-@pytest.mark.parametrize("m,n,k,tile,epilogue,bias", _cases(),
+def _aligned_cases(seed=20261206):
+    """K a multiple of 128 with M and N tails: one case per tile, every epilogue."""
+    rng = np.random.default_rng(seed)
+    out = []
+    for i, tile in enumerate(TILES):
+        m = int(rng.integers(1, 700))
+        n = int(rng.integers(1, 90)) * 8 + (4 if i % 3 == 2 else 0)
+        k = int(rng.integers(1, 12)) * 128
+        out.append((m, n, k, tile, EPILOGUES[i % len(EPILOGUES)], i % 2 == 0))
+    return out
+
+
+@pytest.mark.parametrize("m,n,k,tile,epilogue,bias", _cases() + _aligned_cases(),
                          ids=lambda v: str(v) if not isinstance(v, tuple) else "x".join(map(str, v)))
 def test_random_shape(m, n, k, tile, epilogue, bias):
     g = torch.Generator().manual_seed(m * 1000003 + n * 101 + k)
