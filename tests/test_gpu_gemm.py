@@ -34,6 +34,8 @@ def rand_i8(shape, g):
 @pytest.mark.parametrize("tile", TILES, ids=str)
 @pytest.mark.parametrize("m,n,k", [
     (1, 64, 64), (7, 80, 48), (256, 256, 64), (300, 520, 272), (257, 255, 1024), (129, 384, 5120 + 16),
+    # K of one and two 128-byte k-steps: the operand rings issue DMAs past the last k-step
+    (200, 136, 128), (65, 520, 256),
 ])
 def test_int32_accumulators_bit_exact(m, n, k, tile):
     g = gen(m * 7 + n * 3 + k)
