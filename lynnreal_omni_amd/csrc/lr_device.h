@@ -152,6 +152,17 @@ __device__ __forceinline__ int quant_one(float x, float s, float inv) {
   return (int)(int8_t)(quant_bits(x, s, inv) & 0xffu);
 }
 
+// The same quotient in three operations for rows with absmax < 2^80: with
+// hi = 1/s and lo = fma(-s, hi, 1) * hi, hi + lo is 1/s to about 2^-47
+// relative, and rint(fma(x, hi, x * lo)) equals the clamped rint(fl(x / s))
+// for every bf16 absmax below 2^80 and bf16 x with |x| <= absmax
+// (tests/quant_division_check.c, exhaustive; from absmax 2^125 on lo is
+// subnormal and a few pairs differ).
+__device__ __forceinline__ float quant_lo(float s, float hi) { return __builtin_fmaf(-s, hi, 1.0f) * hi; }
+__device__ __forceinline__ uint32_t quant_bits_split(float x, float hi, float lo) {
+  return __float_as_uint(__builtin_fmaf(x, hi, x * lo) + 0x1.8p23f);
+}
+
 // Low bytes of four words -> one word (three v_perm_b32).
 __device__ __forceinline__ uint32_t low_bytes4(uint32_t a, uint32_t b, uint32_t c, uint32_t d) {
   const uint32_t ab = __builtin_amdgcn_perm(b, a, 0x0c0c0400u);
@@ -164,6 +175,13 @@ __device__ __forceinline__ uint2 quant8(const float f[8], float s, float inv) {
   uint32_t t[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) t[e] = quant_bits(f[e], s, inv);
+  return make_uint2(low_bytes4(t[0], t[1], t[2], t[3]), low_bytes4(t[4], t[5], t[6], t[7]));
+}
+
+__device__ __forceinline__ uint2 quant8_split(const float f[8], float hi, float lo) {
+  uint32_t t[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) t[e] = quant_bits_split(f[e], hi, lo);
   return make_uint2(low_bytes4(t[0], t[1], t[2], t[3]), low_bytes4(t[4], t[5], t[6], t[7]));
 }
 

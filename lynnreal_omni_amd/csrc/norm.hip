@@ -376,13 +376,24 @@ __device__ __forceinline__ void norm_row_f32(const NormArgs& p, int64_t row, con
     __builtin_amdgcn_sched_barrier(0);
   }
   if (QUANT) {
-    const float s = quant_scale(wave_max(amax));
+    const float rmax = wave_max(amax);
+    const float s = quant_scale(rmax);
     const float inv = 1.0f / s;
     const auto qrow = row_rsrc(p.q + row * H, H);
+    // Rows below 2^80 (all real activations) take the three-operation quotient.
+    if (__builtin_amdgcn_readfirstlane(rmax < 0x1p80f ? 1 : 0)) {
+      const float lo = quant_lo(s, inv);
 #pragma unroll
-    for (int m = 0; m < CPL; ++m) {
-      buf_store8(qrow, 8u * lane, 512u * m, quant8(f[m], s, inv));
-      __builtin_amdgcn_sched_barrier(0);
+      for (int m = 0; m < CPL; ++m) {
+        buf_store8(qrow, 8u * lane, 512u * m, quant8_split(f[m], inv, lo));
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    } else {
+#pragma unroll
+      for (int m = 0; m < CPL; ++m) {
+        buf_store8(qrow, 8u * lane, 512u * m, quant8(f[m], s, inv));
+        __builtin_amdgcn_sched_barrier(0);
+      }
     }
     if (lane == 0) p.scales[row] = s;
   } else {
