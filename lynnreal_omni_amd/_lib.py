@@ -56,7 +56,6 @@ SIGNATURES = {
     "lr_adaln_table": [_P, _I32, _I32, _P, _P, _P, _I64, _I64, _I64, _P],
     "lr_device_supported": [_I32],
     "lr_abi_version": [],
-    "lr_gemm_set_group_m": [_I32],
 }
 
 _lock = threading.Lock()
@@ -125,6 +124,15 @@ def check_device(t: torch.Tensor) -> None:
     if not ok:
         raise RuntimeError(f"device {index} ({torch.cuda.get_device_name(index)}) is not supported: "
                            "liblynnreal_amd.so is built for gfx950 only")
+
+
+def same_device(primary: torch.Tensor, **tensors) -> None:
+    """Raise ValueError unless every tensor given (None is skipped) lives on
+    `primary`'s device. The kernels receive raw pointers, so a host tensor or
+    one on another GPU must be refused here, before any launch."""
+    for name, t in tensors.items():
+        if t is not None and t.device != primary.device:
+            raise ValueError(f"{name} is on {t.device}, but the kernel runs on {primary.device}")
 
 
 def stream(t: torch.Tensor) -> int:

@@ -43,6 +43,10 @@
 #ifndef GEMM_SETPRIO
 #define GEMM_SETPRIO 1
 #endif
+// Rows of tiles per raster group of the XCD-aware tile order.
+#ifndef GEMM_GROUP_M
+#define GEMM_GROUP_M 8
+#endif
 
 namespace lr {
 namespace {
@@ -773,8 +777,6 @@ int auto_tile(int64_t m, int64_t n) {
 
 using namespace lr;
 
-static int g_group_m_override = 0;
-
 extern "C" int lr_int8_gemm(const int8_t* a, const int8_t* b, int64_t b_stride_k,
                             int64_t b_stride_n, int64_t m, int64_t n, int64_t k,
                             const float* row_scale, const float* col_scale, const void* bias,
@@ -803,7 +805,7 @@ extern "C" int lr_int8_gemm(const int8_t* a, const int8_t* b, int64_t b_stride_k
   p.indices = indices; p.m = m; p.n = n; p.k = k; p.b_sk = b_stride_k; p.b_sn = b_stride_n;
   p.table_rows = table_rows; p.table_width = table_width; p.sequence = sequence;
   p.gate_slot = gate_slot;
-  p.group_m = g_group_m_override > 0 ? g_group_m_override : 8;
+  p.group_m = GEMM_GROUP_M;
   p.nvec = n % 4 == 0 && aligned(c, epilogue == LR_EPI_RAW_INT32 ? 16 : 8) &&
            (epilogue == LR_EPI_RAW_INT32 || aligned(col_scale, 16)) &&
            (bias == nullptr || aligned(bias, 8)) &&
@@ -836,11 +838,4 @@ extern "C" int lr_int8_gemm(const int8_t* a, const int8_t* b, int64_t b_stride_k
     default: dispatch_bias<EPI_RAW>(!fast, tile, false, p, st); break;
   }
   return check_launch("int8_gemm");
-}
-
-// Tuning hook: rows of tiles per raster group (0 = default 8).
-extern "C" int lr_gemm_set_group_m(int group_m) {
-  LR_REQUIRE(group_m >= 0 && group_m <= 64, "group_m out of range");
-  g_group_m_override = group_m;
-  return LR_OK;
 }

@@ -85,6 +85,8 @@ def int8_matmul(a, b, row_scale, column_scale, bias=None, *, tile=None, activati
     if a.dtype != torch.int8 or b.dtype != torch.int8 or not a.is_contiguous() or a.shape[1] != b.shape[0]:
         raise ValueError("INT8 GEMM requires contiguous row-major activations and compatible INT8 weights")
     _lib.check_device(a)
+    _lib.same_device(a, b=b, row_scale=row_scale, column_scale=column_scale, bias=bias,
+                     residual=residual, table=table, indices=indices)
     m, k = a.shape
     n = b.shape[1]
     row_scale = row_scale.reshape(-1).float().contiguous()
@@ -131,5 +133,6 @@ def int8_matmul_int32(a, b, *, tile=None):
     if a.dtype != torch.int8 or b.dtype != torch.int8 or not a.is_contiguous() or a.shape[1] != b.shape[0]:
         raise ValueError("INT8 GEMM requires contiguous row-major activations and compatible INT8 weights")
     _lib.check_device(a)
+    _lib.same_device(a, b=b)
     out = torch.empty((a.shape[0], b.shape[1]), device=a.device, dtype=torch.int32)
     return _launch(a, b, None, None, None, out, _lib.EPI_RAW_INT32, tile)

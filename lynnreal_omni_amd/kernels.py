@@ -45,6 +45,7 @@ def _norm_args(source, norm, table, indices):
     weight = getattr(norm, "weight", None)
     if weight is None:
         raise ValueError("norm must have a weight")
+    _lib.same_device(source, **{"norm.weight": weight}, table=table, indices=indices)
     weight = _bf16(weight, "norm.weight")
     table = _bf16(table, "table")
     indices = indices.reshape(-1).contiguous()
@@ -79,6 +80,8 @@ def int8_epilogue(accumulator, activation_scale, weight_scale, bias):
         raise ValueError("accumulator must be int32")
     accumulator = accumulator.contiguous()
     _lib.check_device(accumulator)
+    _lib.same_device(accumulator, activation_scale=activation_scale, weight_scale=weight_scale,
+                     bias=bias)
     width = accumulator.shape[-1]
     rows = accumulator.numel() // width if width else 0
     a_scale = activation_scale.reshape(-1).float().contiguous()
@@ -127,6 +130,7 @@ def residual_rms_quant(source, update, norm, table, indices):
     source, weight, table, indices, hidden, sequence, width, table_rows = _norm_args(
         source, norm, table, indices)
     update = _bf16(update, "update")
+    _lib.same_device(source, update=update)
     if update.shape != source.shape:
         raise ValueError("update must have the shape of source")
     rows = source.numel() // hidden
@@ -144,6 +148,7 @@ def _gated_residual(residual, update, table, indices, gate_slot):
     """residual + gate * update with per-token gate (model/kernels.py:292-304)."""
     residual = _bf16(residual, "residual")
     _lib.check_device(residual)
+    _lib.same_device(residual, update=update, table=table, indices=indices)
     update = _bf16(update, "update")
     if update.shape != residual.shape:
         raise ValueError("update must have the shape of residual")
@@ -223,6 +228,10 @@ def qk_norm_rope(query, key, query_weight, key_weight, rotary_emb, eps):
         if t.dtype != torch.bfloat16:
             raise ValueError(f"{name} must be bfloat16, got {t.dtype}")
     _lib.check_device(query)
+    _lib.same_device(query, key=key, query_weight=query_weight, key_weight=key_weight, cos=cos, sin=sin)
+    if query_weight.numel() != head_dim or key_weight.numel() != head_dim:
+        raise ValueError(f"query/key norm weights must have head_dim={head_dim} entries, got "
+                         f"{query_weight.numel()} and {key_weight.numel()}")
 
     def rows(t):
         # Element (b, t, h, d) must sit at b*S*token_stride + t*token_stride + h*head_stride + d.
@@ -263,6 +272,7 @@ def adaln_table(temb, weight, bias=None, *, silu=True):
         raise ValueError(f"temb must be float32 or bfloat16, got {temb.dtype}")
     weight = _bf16(weight, "weight")
     _lib.check_device(weight)
+    _lib.same_device(weight, temb=temb, bias=bias)
     out_features, in_features = weight.shape
     if temb.shape[-1] != in_features:
         raise ValueError(f"temb has {temb.shape[-1]} features, the weight expects {in_features}")
