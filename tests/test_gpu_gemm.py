@@ -119,14 +119,17 @@ def test_reference_install_check_shapes(shape):
     assert hashlib.sha256(y.tobytes()).hexdigest() == want["y_sha256"]
 
 
-def test_north_star_shape_sampled_rows():
-    """M=12288, K=5120, N=20480: the whole int32 product against torch's own
-    GPU int8 GEMM when it runs here, and sampled rows against the oracle."""
+def test_north_star_shape_whole_product():
+    """M=12288, K=5120, N=20480: the whole int32 product equals torch._int_mm
+    on the GPU (hipBLASLt's INT8 GEMM, an independent implementation whose
+    results are exact integers), sampled rows equal the C oracle, and every
+    row sum equals its closed form by linearity."""
     g = gen(14)
     m, n, k = 12288, 20480, 5120
     a = torch.randint(-127, 128, (m, k), dtype=torch.int8, generator=g).cuda()
     w = torch.randint(-127, 128, (n, k), dtype=torch.int8, generator=g).cuda()
     acc = int8_gemm.int8_matmul_int32(a, w.t())
+    assert torch.equal(acc, torch._int_mm(a, w.t()))
     rows = torch.cat([torch.arange(0, 64), torch.randint(64, m - 64, (64,), generator=g),
                       torch.arange(m - 64, m)])
     got = acc[rows.cuda()].cpu().numpy()

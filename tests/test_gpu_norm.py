@@ -99,3 +99,49 @@ def test_ragged_c5_per_token_modulation():
     res, q, s = gpu.residual_rms_quant(x, u, w, table, idx, 1e-6)
     rr, rq, rs = ref.residual_rms_quant(x, u, w, table, idx, 1e-6)
     assert np.array_equal(res, rr) and np.array_equal(q, rq) and np.array_equal(s, rs)
+
+
+BIG = 0x6A80   # bf16 2^86: rows modulated by it have |y| far above 2^80
+
+
+@pytest.mark.parametrize("kernel", ["rms_adaln_quant", "residual_rms_quant"])
+def test_quantizer_branch_for_huge_rows_one_table_row(kernel):
+    """Rows whose modulated absmax is at or above 2^80 take the corrected
+    quotient; the rest take the three-operation one. One table row whose scale
+    slots are 2^86 makes every nonzero row huge, while all-zero input rows stay
+    at |y| = |shift|: both branches run in one launch of the one-row path."""
+    x, u, w, table, idx = case(1, 4096, 5120, 1, 21)
+    table[:, 1 * 5120:2 * 5120] = BIG    # scale slot of (0, 1)
+    table[:, 4 * 5120:5 * 5120] = BIG    # scale slot of (3, 4)
+    x[:, ::5] = 0
+    if kernel == "residual_rms_quant":
+        u[:, ::5] = 0
+        res, q, s = gpu.residual_rms_quant(x, u, w, table, idx, 1e-6)
+        rr, rq, rs = ref.residual_rms_quant(x, u, w, table, idx, 1e-6)
+        assert np.array_equal(res, rr)
+    else:
+        q, s = gpu.rms_adaln_quant(x, w, table, idx, 0, 1, 1e-6)
+        rq, rs = ref.rms_adaln_quant(x, w, table, idx, 0, 1, 1e-6)
+    assert (rs[::5] < 2.0 ** 80 / 127).all() and (np.delete(rs, np.s_[::5]) > 2.0 ** 80 / 127).all()
+    assert np.array_equal(q, rq) and np.array_equal(s, rs)
+
+
+@pytest.mark.parametrize("kernel", ["rms_adaln_quant", "residual_rms_quant"])
+def test_quantizer_branch_for_huge_rows_across_frame_runs(kernel):
+    """The C5 per-frame layout with the scale slots of frames 1, 3 and 5 set to
+    2^86: slices that span a frame boundary (two runs of table rows) switch
+    between the two quotient forms inside one slice."""
+    x, u, w, table, idx = case(1, 12605, 5120, 6, 22, True)
+    for frame in (1, 3, 5):
+        table[frame, 1 * 5120:2 * 5120] = BIG
+        table[frame, 4 * 5120:5 * 5120] = BIG
+    if kernel == "residual_rms_quant":
+        res, q, s = gpu.residual_rms_quant(x, u, w, table, idx, 1e-6)
+        rr, rq, rs = ref.residual_rms_quant(x, u, w, table, idx, 1e-6)
+        assert np.array_equal(res, rr)
+    else:
+        q, s = gpu.rms_adaln_quant(x, w, table, idx, 0, 1, 1e-6)
+        rq, rs = ref.rms_adaln_quant(x, w, table, idx, 0, 1, 1e-6)
+    huge = np.isin(idx, (1, 3, 5))
+    assert (rs[huge] > 2.0 ** 80 / 127).all() and (rs[~huge] < 2.0 ** 80 / 127).all()
+    assert np.array_equal(q, rq) and np.array_equal(s, rs)
