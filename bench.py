@@ -22,7 +22,7 @@ Prints ONE JSON line on stdout (details on stderr):
   roofline   the dominant kernel (FFN-up GEMM, M=12288 K=5120 N=20480) against
              the INT8 MFMA dense peak
   cpu_baseline  the reference's torch path (oracle/torch_path.py) on the host
-             cores, on a token slice of the same chain
+             cores, on the same chain at the same size
 """
 from __future__ import annotations
 
@@ -54,13 +54,19 @@ def parse():
     p.add_argument("--tokens", type=int, default=12288)
     p.add_argument("--hidden", type=int, default=5120)
     p.add_argument("--ffn", type=int, default=20480)
-    p.add_argument("--cpu-tokens", type=int, default=256, help="token slice timed on the CPU")
+    p.add_argument("--cpu-tokens", type=int, default=None,
+                   help="tokens of the chain timed on the CPU (default: all of them, the whole config)")
     p.add_argument("--no-cpu-baseline", action="store_true")
-    p.add_argument("--workload", choices=("c3", "c1", "c4", "c5"), default="c3",
+    p.add_argument("--workload", choices=("c3", "c1", "c4", "c5", "rows", "qk", "flash", "adaln"),
+                   default="c3",
                    help="c3: the projection chain (default, the headline line); c1: one W8A8 linear "
                         "(2048x5120 -> 5120) with the CPU torch path beside it; c4: the T=65536 W8A8 FFN "
                         "against the same shapes in bf16; c5: the chain at T=12288+317 with per-frame "
-                        "modulation rows, and M=256 projections")
+                        "modulation rows, and M=256 projections; rows: the HBM-bound row kernels at the "
+                        "C2/C3 shape; qk: QK RMSNorm + RoPE; flash: Flash token selection; adaln: the "
+                        "adaLN table projection")
+    p.add_argument("--flush", action="store_true",
+                   help="rows workload: overwrite the MALL before each launch and time launches one by one")
     p.add_argument("--no-vendor-gemm", dest="vendor_gemm", action="store_false",
                    help="skip the like-for-like FFN-up GEMM comparison with torch._int_mm (hipBLASLt)")
     p.add_argument("--copy-calibration", action="store_true",
@@ -232,7 +238,9 @@ def vendor_comparison(args, a, w_kn, reps=10):
 
 
 def run_cpu(args, data):
-    """The reference's torch path on the host cores, on a token slice."""
+    """The reference's torch path on the host cores: the whole chain of the
+    same config (or its first --cpu-tokens tokens), one untimed pass, then the
+    median of 3 to 5 timed passes within a ~30 s budget."""
     import torch
     from oracle import torch_path as tp
 
@@ -240,7 +248,7 @@ def run_cpu(args, data):
     cap = int(os.environ.get("OMP_NUM_THREADS", cores) or cores)
     threads = max(1, min(cores, cap))
     torch.set_num_threads(threads)
-    n = min(args.cpu_tokens, args.tokens)
+    n = min(args.cpu_tokens or args.tokens, args.tokens)
     x = data.x[:, :n].contiguous()
     attn = data.attn[:, :n].contiguous()
     weights = {"qkv": data.weights["qkv"], "out": data.weights["out"], "up": data.weights["up"],
@@ -254,16 +262,18 @@ def run_cpu(args, data):
     once()
     times = []
     budget = time.perf_counter()
-    while len(times) < 5 and (time.perf_counter() - budget < 20 or len(times) < 2):
+    while len(times) < 5 and (time.perf_counter() - budget < 30 or len(times) < 3):
         t = time.perf_counter()
         once()
         times.append(time.perf_counter() - t)
     med = statistics.median(times)
     ops = sum(gemm_ops(n, args.hidden, args.ffn).values())
     return {"value": round(ops / med / 1e12, 4), "unit": "TOPS", "cores": threads, "kind": "port",
-            "sample": f"first {n} of {args.tokens} tokens of the same chain, all four projections at "
-                      f"full width; torch CPU ops (torch._int_mm) restating model/int8.py:60-68 and "
-                      f"model/kernels.py; median of {len(times)} reps ({med * 1e3:.1f} ms/rep)",
+            "sample": (f"the whole C3 chain ({n} tokens)" if n == args.tokens else
+                       f"first {n} of {args.tokens} tokens of the same chain") +
+                      f", all four projections at full width; torch CPU ops (torch._int_mm) restating "
+                      f"model/int8.py:60-68 and model/kernels.py; median of {len(times)} reps "
+                      f"({med * 1e3:.1f} ms/rep)",
             "cpu": _cpu_name()}
 
 
@@ -472,6 +482,183 @@ def run_c4(args):
     }
 
 
+def _timed_launches(fn, iters, flush=None):
+    """Average us per call of `fn` between two HIP events on the current stream
+    (back-to-back calls). With `flush` (a 1 GiB buffer) the 256 MB MALL is
+    overwritten before every call and each call is timed alone: the median,
+    with inputs cold in every cache."""
+    import torch
+    for _ in range(5):
+        fn()
+    stream = torch.cuda.current_stream()
+    torch.cuda.synchronize()
+    if flush is None:
+        start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        for _ in range(iters):
+            fn()
+        stop.record(stream)
+        stop.synchronize()
+        return start.elapsed_time(stop) * 1e3 / iters
+    times = []
+    for _ in range(iters):
+        flush.zero_()
+        start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        fn()
+        stop.record(stream)
+        stop.synchronize()
+        times.append(start.elapsed_time(stop) * 1e3)
+    return statistics.median(times)
+
+
+def _rate(us, nbytes):
+    gbs = nbytes / (us * 1e-6) / 1e9
+    return {"us": round(us, 2), "bytes": nbytes, "GB/s": round(gbs, 1),
+            "hbm_frac": round(gbs / PEAK_HBM_GBS, 4)}
+
+
+def _side_line(metric, value, unit, args, workload, kernels, **extra):
+    line = {"metric": metric, "value": value, "unit": unit, "n_gpus": 1, "steps": args.steps,
+            "warmup": args.warmup, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+            "dtype": extra.pop("dtype", "bf16"), "data": "synthetic, resident in HBM",
+            "config": {"workload": workload, **extra.pop("config", {})}, "kernels": kernels}
+    line.update(extra)
+    return line
+
+
+def run_rows(args):
+    """The HBM-bound row kernels at the C2/C3 shape (T tokens, D, FFN width):
+    one HIP-event time per kernel (back-to-back launches, or with --flush single
+    launches after a 1 GiB write that evicts the MALL) and the algorithmic HBM
+    rate, bytes being the one pass each kernel makes over its rows:
+      rms_adaln_quant     3 T D + 4 T      (x in, q out, scales)
+      rms_adaln           4 T D            (x in, y out)
+      residual_rms_quant  7 T D + 4 T      (x, u in; x' out; q out; scales)
+      gated_residual      6 T D            (x, u in; out)
+      quantize_rows       3 T K + 4 T
+      swiglu_quant        5 T I + 4 T      (P [T, 2I] in; q [T, I] out; scales)
+    (gamma and the table row are read once per block and not counted). The last
+    entry is torch's own device copy of the FFN-wide rows, a yardstick for a
+    plain streaming kernel on the same box. value = the fused norm + modulate +
+    quantize prologue's GB/s."""
+    import torch
+    from lynnreal_omni_amd import kernels as k
+
+    t, d, f = args.tokens, args.hidden, args.ffn
+    g = torch.Generator(device="cuda").manual_seed(3)
+    x = torch.randn(1, t, d, device="cuda", generator=g).bfloat16()
+    u = torch.randn(1, t, d, device="cuda", generator=g).bfloat16()
+    h = torch.randn(t, f, device="cuda", generator=g).bfloat16()
+    table = (0.1 * torch.randn(1, 6 * d, device="cuda", generator=g)).bfloat16()
+    idx = torch.zeros(t, dtype=torch.int64, device="cuda")
+    norm = types.SimpleNamespace(weight=(1 + 0.05 * torch.randn(d, device="cuda", generator=g)).bfloat16(),
+                                 eps=1e-6)
+    h2 = torch.empty_like(h)
+    cases = [
+        ("rms_adaln_quant", lambda: k._rms_adaln_quant_int8(x, norm, table, idx, 0, 1), 3 * t * d + 4 * t),
+        ("rms_adaln", lambda: k._rms_adaln(x, norm, table, idx, 0, 1), 4 * t * d),
+        ("residual_rms_quant", lambda: k.residual_rms_quant(x, u, norm, table, idx), 7 * t * d + 4 * t),
+        ("gated_residual", lambda: k._gated_residual(x, u, table, idx, 2), 6 * t * d),
+        (f"quantize_rows_k{d}", lambda: k.quantize_rows(x.view(t, d)), 3 * t * d + 4 * t),
+        (f"quantize_rows_k{f}", lambda: k.quantize_rows(h), 3 * t * f + 4 * t),
+        (f"swiglu_quant_i{f // 2}", lambda: k._swiglu_quant_int8(h), 5 * t * (f // 2) + 4 * t),
+        ("torch_copy_reference", lambda: h2.copy_(h), 4 * t * f),
+    ]
+    flush = torch.empty(1 << 30, dtype=torch.uint8, device="cuda") if args.flush else None
+    iters = max(args.steps, 20)
+    out = {name: _rate(_timed_launches(fn, iters, flush), nbytes) for name, fn, nbytes in cases}
+    return _side_line("fused RMSNorm + adaLN + INT8 quant GB/s (row kernels)",
+                      out["rms_adaln_quant"]["GB/s"], "GB/s", args, "row kernels (C2/C3 shapes)", out,
+                      config={"tokens": t, "hidden": d, "ffn": f, "cold_caches": bool(args.flush)},
+                      iters=iters)
+
+
+def run_qk(args):
+    """Fused Q/K RMSNorm + RoPE at the C2 shape: Q and K are strided views of a
+    fused QKV output [1, T, 3 * 40, 128], as model/fusion.py:22-30 produces them,
+    full-width rotary. Bytes = 8 * rows * head_dim (Q, K read; Q, K written, bf16)
+    + 8 * T * rotary_dim (fp32 cos and sin); the bare norm (rotary 0) beside it."""
+    import torch
+    from lynnreal_omni_amd import kernels
+
+    heads, head_dim, t = 40, 128, args.tokens
+    g = torch.Generator().manual_seed(20261201)
+    qkv = torch.randn(1, t, 3 * heads, head_dim, generator=g).bfloat16().cuda()
+    q, key = qkv[:, :, :heads], qkv[:, :, heads:2 * heads]
+    w = (1 + 0.05 * torch.randn(2, head_dim, generator=g)).bfloat16().cuda()
+    out = {}
+    for rotary in (head_dim, 0):
+        phase = torch.randn(t, rotary, generator=g).cuda()
+        rope = (phase.cos(), phase.sin())
+        us = _timed_launches(lambda: kernels.qk_norm_rope(q, key, w[0], w[1], rope, 1e-6),
+                             max(args.steps, 100))
+        out[f"qk_norm_rope_rotary{rotary}"] = _rate(us, 8 * t * heads * head_dim + 8 * t * rotary)
+    return _side_line("QK RMSNorm + RoPE GB/s", out[f"qk_norm_rope_rotary{head_dim}"]["GB/s"], "GB/s",
+                      args, "QK norm + RoPE (C2 shape)", out,
+                      config={"tokens": t, "heads": heads, "head_dim": head_dim})
+
+
+def run_flash(args):
+    """Flash token selection on a C5 layout: 317 text rows, then 6 frames of a
+    32 x 64 video grid, hidden 5120. spatial_layout (torch bookkeeping + the
+    nearest-anchor kernel), the row gather (bytes 2 * 2 * kept * D) and the fused
+    restore (2 * T * D full + 2 * 2 * kept * D + 2 * T * D out)."""
+    import torch
+    from lynnreal_omni_amd import flash
+
+    frames, height, width, text, hidden = 6, 32, 64, 317, args.hidden
+    t_h = torch.arange(frames, dtype=torch.float64).repeat_interleave(height * width)
+    hh = torch.arange(height, dtype=torch.float64).repeat_interleave(width).repeat(frames)
+    ww = torch.arange(width, dtype=torch.float64).repeat(frames * height)
+    video = torch.stack([t_h, hh, ww], 1)
+    txt = torch.stack([torch.arange(text, dtype=torch.float64), torch.zeros(text), torch.zeros(text)], 1)
+    pos = torch.cat([txt, video]).cuda()
+    tags = torch.cat([torch.ones(text, dtype=torch.long), torch.zeros(video.shape[0], dtype=torch.long)]).cuda()
+    tokens = pos.shape[0]
+    keep, inverse = flash.spatial_layout(pos, tags)
+    kept = keep.numel()
+    g = torch.Generator(device="cuda").manual_seed(1)
+    full = torch.randn(1, tokens, hidden, device="cuda", generator=g).bfloat16()
+    cur = torch.randn(1, kept, hidden, device="cuda", generator=g).bfloat16()
+    inp = torch.randn(1, kept, hidden, device="cuda", generator=g).bfloat16()
+    iters = max(args.steps, 50)
+    out = {"spatial_layout": {"us": round(_timed_launches(lambda: flash.spatial_layout(pos, tags),
+                                                           max(5, iters // 10)), 1)},
+           "gather_rows": _rate(_timed_launches(lambda: flash.gather_rows(full, keep, 1), iters),
+                                4 * kept * hidden),
+           "restore": _rate(_timed_launches(lambda: flash.restore(full, cur, inp, inverse, 1.0), iters),
+                            4 * tokens * hidden + 4 * kept * hidden)}
+    return _side_line("Flash restore GB/s", out["restore"]["GB/s"], "GB/s", args,
+                      "Flash token selection (C5 layout)", out,
+                      config={"tokens": tokens, "kept": kept, "hidden": hidden})
+
+
+def run_adaln(args):
+    """The adaLN table linear(F.silu(temb).to(bf16)) through lr_adaln_table for
+    M = 1 and 6 time rows, K = 5120, N = 6 * 5120, against the same expression
+    in torch (F.silu, then F.linear on hipBLASLt). Bytes = 2 * N * K (the
+    weight, read once)."""
+    import torch
+    import torch.nn.functional as F
+    from lynnreal_omni_amd import kernels
+
+    kk, n = args.hidden, 6 * args.hidden
+    g = torch.Generator(device="cuda").manual_seed(2)
+    w = (0.02 * torch.randn(n, kk, device="cuda", generator=g)).bfloat16()
+    b = (0.1 * torch.randn(n, device="cuda", generator=g)).bfloat16()
+    out = {}
+    iters = max(args.steps, 100)
+    for m in (1, 6):
+        temb = torch.randn(m, kk, device="cuda", generator=g)
+        row = _rate(_timed_launches(lambda: kernels.adaln_table(temb, w, b), iters), 2 * n * kk)
+        row["torch_silu_linear_us"] = round(_timed_launches(
+            lambda: F.linear(F.silu(temb).to(torch.bfloat16), w, b), iters), 2)
+        out[f"adaln_table_m{m}"] = row
+    return _side_line("adaLN table GB/s (M=1)", out["adaln_table_m1"]["GB/s"], "GB/s", args,
+                      "adaLN table projection", out, config={"k": kk, "n": n})
+
+
 def _cpu_name():
     try:
         for line in open("/proc/cpuinfo"):
@@ -500,6 +687,11 @@ def main():
     if args.workload == "c5":
         log(f"device {torch.cuda.get_device_name(0)}; C5 ragged chain and M=256 projections")
         print(json.dumps(run_c5(args)), flush=True)
+        return 0
+    side = {"rows": run_rows, "qk": run_qk, "flash": run_flash, "adaln": run_adaln}
+    if args.workload in side:
+        log(f"device {torch.cuda.get_device_name(0)}; workload {args.workload}")
+        print(json.dumps(side[args.workload](args)), flush=True)
         return 0
     if args.workload == "c4":
         if args.tokens == 12288:
@@ -535,7 +727,7 @@ def main():
     log(json.dumps({"kernels": detail, "wall_ms_per_step": wall * 1e3 / args.steps}, indent=1))
     cpu = None
     if not args.no_cpu_baseline:
-        log(f"cpu baseline on {args.cpu_tokens} tokens ...")
+        log(f"cpu baseline on {args.cpu_tokens or args.tokens} tokens ...")
         cpu = run_cpu(args, data)
     line = {
         "metric": "INT8 GEMM TOPS (% INT8 MFMA peak) + fused DiT-block projection us at M=12288",
@@ -560,7 +752,7 @@ def main():
         "kernels": detail,
         "roofline": {"kernel": "int8 GEMM FFN-up M=12288 K=5120 N=20480 (+GELU epilogue)",
                      "bound": "mfma", "achieved": round(up_tops, 1), "peak": PEAK_INT8_TOPS,
-                     "unit": "TFLOP/s", "frac": round(up_tops / PEAK_INT8_TOPS, 4),
+                     "unit": "TOPS", "frac": round(up_tops / PEAK_INT8_TOPS, 4),
                      "traffic": traffic_bytes("up"), "us": round(up_us, 2)},
         "cpu_baseline": cpu,
         "vendor_int8_gemm": vendor,
