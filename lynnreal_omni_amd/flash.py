@@ -62,6 +62,7 @@ def restore(full: torch.Tensor, current: torch.Tensor, input: torch.Tensor,
     (model/flash.py:83-84) does.
     """
     _lib.check_device(full)
+    _lib.same_device(full, current=current, input=input)
     for name, t in (("full", full), ("current", current), ("input", input)):
         if t.dtype != torch.bfloat16:
             raise ValueError(f"{name} must be bfloat16, got {t.dtype}")
@@ -82,22 +83,24 @@ def restore(full: torch.Tensor, current: torch.Tensor, input: torch.Tensor,
     return out
 
 
-def _retained(values: torch.Tensor, stride: int) -> torch.Tensor:
-    """Every stride-th distinct value in increasing order, and always the largest."""
-    alphabet = torch.unique(values, sorted=True)
-    picked = alphabet[::stride]
-    if picked[-1] != alphabet[-1]:
-        picked = torch.cat((picked, alphabet[-1:]))
-    return picked
+def _on_grid(coordinate: torch.Tensor, alphabet: torch.Tensor, stride: int) -> torch.Tensor:
+    """Whether each coordinate (a member of the sorted `alphabet` of distinct
+    values) is every stride-th distinct value counting from the smallest, or
+    the largest one: its rank in the alphabet decides."""
+    rank = torch.searchsorted(alphabet, coordinate)
+    return (rank % stride == 0) | (rank == alphabet.numel() - 1)
 
 
 def spatial_layout(positions: torch.Tensor, tags: torch.Tensor, stride: int = 2):
     """(keep, inverse) of the Flash selection (model/flash.py:6-33).
 
-    positions [tokens, 3] (time, h, w), tags [tokens] (0 = video). keep: the
-    kept row numbers in increasing order; inverse [tokens]: for a kept row
-    its place in keep, for a dropped video row the place of its nearest kept
-    video row of the same time (fp32 coordinates, first one on ties).
+    positions [tokens, 3] (time, h, w), tags [tokens] (0 = video). A video row
+    is kept when both its h and w are on the stride grid of the video rows'
+    distinct values (the largest value always counts); every other row is
+    kept. keep: the kept row numbers in increasing order. inverse [tokens]: a
+    kept row's place in keep; a dropped row's is its nearest kept video row
+    of the same time (fp32 coordinates, first one on ties), found by the
+    nearest-anchor kernel.
     """
     if positions.ndim != 2 or tags.ndim != 1 or positions.shape != (tags.numel(), 3):
         raise ValueError("Flash requires a single shared packed layout")
@@ -105,17 +108,18 @@ def spatial_layout(positions: torch.Tensor, tags: torch.Tensor, stride: int = 2)
     if not bool(video.any()):
         raise ValueError("Flash requires video tokens")
     _lib.check_device(positions)
-    on_grid = torch.ones_like(video)
+    _lib.same_device(positions, tags=tags)
+    grid = video.clone()
+    rows = positions[video]
     for axis in (1, 2):
-        column = positions[:, axis]
-        on_grid &= torch.isin(column, _retained(column[video], stride))
-    kept = ~video | on_grid
+        grid[video] &= _on_grid(rows[:, axis], torch.unique(rows[:, axis], sorted=True), stride)
+    kept = ~video | grid
     keep = kept.nonzero().flatten()
-    inverse = torch.empty(tags.shape, dtype=torch.long, device=positions.device)
-    inverse[keep] = torch.arange(keep.numel(), device=positions.device)
-    dropped = (video & ~kept).nonzero().flatten()
-    anchors = (video & kept).nonzero().flatten()
+    # a kept row's place among the kept rows is the running count of kept rows before it
+    inverse = torch.cumsum(kept, 0) - 1
+    dropped = (~kept).nonzero().flatten()
     if dropped.numel():
+        anchors = grid.nonzero().flatten()
         coords = positions.to(torch.float32).contiguous()
         _lib.call("lr_flash_nearest_anchor", coords.data_ptr(), coords.shape[0], dropped.data_ptr(),
                   dropped.numel(), anchors.data_ptr(), anchors.numel(), inverse.data_ptr(),
@@ -123,19 +127,78 @@ def spatial_layout(positions: torch.Tensor, tags: torch.Tensor, stride: int = 2)
     return keep, inverse
 
 
-def _check_config(blocks, config):
-    compression = config["token_compression"]
+# The one token layout the trained Flash blocks support: spatial selection with
+# stride 2, every text and audio row kept, no refresh blocks. Each entry is
+# (key, value when absent or None to require the key, test).
+_LAYOUT_RULES = (
+    ("reduction", None, lambda v: v == "select"),
+    ("spatial_stride", None, lambda v: v == 2),
+    ("preserve_text_tokens", None, bool),
+    ("preserve_audio_tokens", None, bool),
+    ("full_refresh_blocks", False, lambda v: not v),
+    ("text_stride", 1, lambda v: v == 1),
+    ("audio_stride", 1, lambda v: v == 1),
+)
+
+
+def _compressed_span(blocks, config):
+    """Blocks [start, end) that run on the kept rows, and the restore gain."""
     if len(blocks) != config["num_layers"]:
         raise ValueError("Flash depth and exported weights disagree")
-    if (compression["reduction"] != "select" or compression["spatial_stride"] != 2
-            or not compression["preserve_text_tokens"] or not compression["preserve_audio_tokens"]
-            or compression.get("full_refresh_blocks")
-            or compression.get("text_stride", 1) != 1 or compression.get("audio_stride", 1) != 1):
-        raise ValueError("unsupported Flash token layout")
-    start, end = compression["full_prefix_blocks"], len(blocks) - compression["full_suffix_blocks"]
+    compression = config["token_compression"]
+    for key, absent, test in _LAYOUT_RULES:
+        value = compression[key] if absent is None else compression.get(key, absent)
+        if not test(value):
+            raise ValueError("unsupported Flash token layout")
+    start = compression["full_prefix_blocks"]
+    end = len(blocks) - compression["full_suffix_blocks"]
     if not 0 < start < end < len(blocks):
         raise ValueError("Flash requires nonempty full-resolution prefix and suffix")
-    return compression, start, end
+    return start, end, float(compression.get("residual_gain", 1.0))
+
+
+class _FlashForward:
+    """Hook state of one Flash transformer: the layout of the current forward
+    (cached across forwards with equal positions and tags) and, between the
+    first compressed block and the restore, the full-resolution hidden rows
+    and the compressed rows that entered the compressed span."""
+
+    def __init__(self, transformer, gain):
+        self.signature = inspect.signature(transformer.forward)
+        self.gain = gain
+        self.layout = None          # (positions, tags, keep, inverse) of the last layout built
+        self.current = None         # (keep, inverse) while a forward runs
+        self.full = self.entered = None
+
+    def begin(self, module, args, kwargs):
+        if module.training or torch.is_grad_enabled():
+            raise ValueError("Flash hooks require frozen inference")
+        if self.current is not None:
+            raise RuntimeError("Flash transformer does not support concurrent forwards")
+        bound = self.signature.bind(*args, **kwargs).arguments
+        positions, tags = bound["position_ids"], bound["token_tags"]
+        cached = self.layout
+        if cached is None or not (torch.equal(positions, cached[0]) and torch.equal(tags, cached[1])):
+            cached = self.layout = (positions.clone(), tags.clone(), *spatial_layout(positions, tags))
+        self.current = cached[2:]
+
+    def compress(self, module, args):
+        hidden, temb, indices, rotary, mask = args
+        keep = self.current[0]
+        if self.full is None:           # the first compressed block: drop rows once
+            self.full, hidden = hidden, gather_rows(hidden, keep, 1)
+            self.entered = hidden
+        return (hidden, temb, gather_rows(indices, keep, 0),
+                tuple(gather_rows(value, keep, -2) for value in rotary),
+                None if mask is None else gather_rows(mask, keep, -1))
+
+    def restore(self, module, args):
+        hidden = restore(self.full, args[0], self.entered, self.current[1], self.gain)
+        self.full = self.entered = None
+        return (hidden, *args[1:])
+
+    def finish(self, *_):
+        self.current = self.full = self.entered = None
 
 
 def configure_flash(transformer, config):
@@ -145,50 +208,16 @@ def configure_flash(transformer, config):
     restored full sequence. The block pre-hook arguments are (hidden, temb,
     adaLN indices, rotary (cos, sin), attention mask), as in the reference;
     hidden/indices/rotary/mask are gathered on their token dimension (1, 0,
-    -2, -1). The hooks keep one forward's state at a time.
+    -2, -1). One forward runs at a time.
     """
     blocks = transformer.transformer_blocks
-    compression, start, end = _check_config(blocks, config)
+    start, end, gain = _compressed_span(blocks, config)
     if hasattr(transformer, "_lynnreal_flash_hooks"):
         raise ValueError("Flash is already configured")
     transformer.h3_token_compression = None
-    signature = inspect.signature(transformer.forward)
-    gain = float(compression.get("residual_gain", 1.0))
-    state: dict = {}
-    cache: dict = {}
-
-    def begin(module, args, kwargs):
-        if module.training or torch.is_grad_enabled():
-            raise ValueError("Flash hooks require frozen inference")
-        if state:
-            raise RuntimeError("Flash transformer does not support concurrent forwards")
-        bound = signature.bind(*args, **kwargs).arguments
-        positions, tags = bound["position_ids"], bound["token_tags"]
-        if not cache or not (torch.equal(positions, cache["positions"]) and torch.equal(tags, cache["tags"])):
-            keep, inverse = spatial_layout(positions, tags)
-            cache.update(positions=positions.clone(), tags=tags.clone(), keep=keep, inverse=inverse)
-        state["keep"], state["inverse"] = cache["keep"], cache["inverse"]
-
-    def compress(module, args):
-        hidden, temb, indices, rotary, mask = args
-        keep = state["keep"]
-        if "full" not in state:
-            state["full"] = hidden
-            hidden = gather_rows(hidden, keep, 1)
-            state["input"] = hidden
-        return (hidden, temb, gather_rows(indices, keep, 0),
-                tuple(gather_rows(value, keep, -2) for value in rotary),
-                None if mask is None else gather_rows(mask, keep, -1))
-
-    def restore_hook(module, args):
-        hidden = restore(state.pop("full"), args[0], state.pop("input"), state["inverse"], gain)
-        return (hidden, *args[1:])
-
-    def finish(*_):
-        state.clear()
-
-    handles = [transformer.register_forward_pre_hook(begin, with_kwargs=True)]
-    handles += [block.register_forward_pre_hook(compress) for block in blocks[start:end]]
-    handles += [blocks[end].register_forward_pre_hook(restore_hook),
-                transformer.register_forward_hook(finish, always_call=True)]
+    run = _FlashForward(transformer, gain)
+    handles = [transformer.register_forward_pre_hook(run.begin, with_kwargs=True)]
+    handles += [block.register_forward_pre_hook(run.compress) for block in blocks[start:end]]
+    handles += [blocks[end].register_forward_pre_hook(run.restore),
+                transformer.register_forward_hook(run.finish, always_call=True)]
     transformer._lynnreal_flash_hooks = handles
