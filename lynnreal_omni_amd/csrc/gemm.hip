@@ -518,97 +518,95 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_fast(GemmArgs p) 
 #pragma unroll
     for (int j = 0; j < FN; ++j) acc[i][j] = v4i{0, 0, 0, 0};
 
-  // At the barrier of k-step kt the slots of k-step kt-1 are free; the
-  // shallower ring's next k-step is issued first, then the deeper ring's.
-  // Each wave's DMAs complete in issue order, so when k-step kt starts only
-  // the deeper ring's newest k-step may still be in flight.
-  // Every k-step issues the shallower ring's next k-step first (first half)
-  // and the deeper ring's second (both rings in that order when equal), and
-  // the prologue issues its k-steps in the same interleaved order. At the
-  // barrier of k-step kt, the DMAs still allowed in flight are those issued
-  // after both A(kt) and B(kt):
-  //   B first: min((NA - 2)(A + B), (NB - 2)(A + B) + A) loads per wave,
-  //   A first: min((NB - 2)(A + B), (NA - 2)(A + B) + B).
+  // One barrier per k-step, between its two halves. Fragments are always read
+  // one half ahead: the second half's while the first half's MFMAs run, and the
+  // next k-step's first half while the second half's MFMAs run, so no MFMA
+  // waits for an LDS read issued after a barrier. At the barrier in k-step kt
+  // every wave has its k-step kt fragments in registers (lgkmcnt(0)), so the
+  // slots of k-step kt are free: the second half refills them with k-step
+  // kt + NA (A) and kt + NB (W), i.e. each ring keeps all of its slots in
+  // flight. The barrier also publishes k-step kt + 1, whose DMAs each wave
+  // has waited for (vmcnt) just before it.
+  //
+  // DMA issue order per wave: round t issues W(t + NB) then A(t + NA) (rounds
+  // -max(NA, NB) .. -1 form the prologue, round t >= 0 is the second half of
+  // k-step t; indices below 0 are skipped). Loads still allowed in flight:
+  //   before k-step 0 (A(0), W(0) landed):     kPro
+  //   at the barrier of k-step kt (A(kt+1), W(kt+1) landed): kMid
   static_assert(NA >= 2 && NB >= 2, "ring depths");
-  constexpr bool kBFirst = NB <= NA;
   constexpr int kStep = A_LOADS + B_LOADS;
-  constexpr int kAfterA = kBFirst ? (NA - 2) * kStep : (NA - 2) * kStep + B_LOADS;
-  constexpr int kAfterB = kBFirst ? (NB - 2) * kStep + A_LOADS : (NB - 2) * kStep;
-  constexpr int kLater = kAfterA < kAfterB ? kAfterA : kAfterB;
-  static_assert(kLater >= 0 && kLater <= 63, "vmcnt range");
-  constexpr int kWait = 0x70 | 0xf00 | (kLater & 0xf) | ((kLater >> 4) << 14);  // vmcnt(kLater)
-  for (int s = 0; s < (NA > NB ? NA : NB) - 1; ++s) {
-    if (kBFirst) {
-      if (s < NB - 1) issue_b(s);
-      if (s < NA - 1) issue_a(s);
-    } else {
-      if (s < NA - 1) issue_a(s);
-      if (s < NB - 1) issue_b(s);
-    }
+  constexpr int kPro = NA > NB ? A_LOADS + (NB - 1) * kStep : (NA - 1) * kStep;
+  constexpr int kMid = NA > NB ? A_LOADS + (NB - 2) * kStep : (NA - 2) * kStep;
+  static_assert(kPro <= 63 && kMid >= 0, "vmcnt range");
+  constexpr int kWaitPro = 0x70 | 0xf00 | (kPro & 0xf) | ((kPro >> 4) << 14);  // vmcnt(kPro)
+  constexpr int kWaitMid = 0x70 | (kMid & 0xf) | ((kMid >> 4) << 14);  // vmcnt(kMid) lgkmcnt(0)
+  constexpr int NMAX = NA > NB ? NA : NB;
+#pragma unroll
+  for (int t = -NMAX; t < 0; ++t) {
+    if (t + NB >= 0) issue_b(t + NB);
+    if (t + NA >= 0) issue_a(t + NA);
   }
-  // One k-step: the first half's fragments are read, then its FM*FN MFMAs run
-  // with the second half's fragment reads and the shallower ring's DMAs
-  // interleaved, then the second half's MFMAs with the deeper ring's DMAs.
-  // Spreading the DMAs over the MFMAs keeps the vector-memory queue from
-  // stalling every wave at once right after the barrier; the scheduling
-  // barriers pin that order.
   constexpr int NMF = FM * FN;
-  constexpr int NR1 = FM + FN;
-  constexpr bool B_FIRST = kBFirst;
-  constexpr int L1 = B_FIRST ? B_LOADS : A_LOADS, L2 = B_FIRST ? A_LOADS : B_LOADS;
+  constexpr int NR = FM + FN;
+  constexpr int ND = A_LOADS + B_LOADS;
+  v4i a0[FM], w0[FN], a1[FM], w1[FN];
+  // Fragment r of a half in MFMA order: a[0], w[0..FN-1], a[1..FM-1] (the
+  // first MFMA needs two reads, each later one at most one new read).
+  auto read_half = [&](const char* sa, const char* sb, int h, int r, v4i (&av)[FM], v4i (&wv)[FN]) {
+    if (r == 0) av[0] = frag(sa, wm * FM, h);
+    else if (r <= FN) wv[r - 1] = frag(sb, wn * FN + r - 1, h);
+    else av[r - FN] = frag(sa, wm * FM + r - FN, h);
+  };
+  __builtin_amdgcn_s_waitcnt(kWaitPro);
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int r = 0; r < NR; ++r) read_half(a_ring, b_ring, 0, r, a0, w0);
+  __builtin_amdgcn_sched_barrier(0);
+
   for (int kt = 0; kt < KT; ++kt) {
-    __builtin_amdgcn_s_waitcnt(kWait);
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
-    __builtin_amdgcn_sched_barrier(0);
     const char* sa = a_ring + (kt % NA) * A_BYTES;
     const char* sb = b_ring + (kt % NB) * B_BYTES;
-    const int kt_b = kt + NB - 1, kt_a = kt + NA - 1;
-    v4i a0[FM], w0[FN], a1[FM], w1[FN];
-    // Read in MFMA order (a0[0], then the W fragments, then a0[1..]): the
-    // first MFMA waits for two reads, not for all of them, while every wave
-    // of the block is reading at once right after the barrier.
-    a0[0] = frag(sa, wm * FM, 0);
-#pragma unroll
-    for (int j = 0; j < FN; ++j) {
-      w0[j] = frag(sb, wn * FN + j, 0);
-      __builtin_amdgcn_sched_barrier(0);
-    }
-#pragma unroll
-    for (int i = 1; i < FM; ++i) a0[i] = frag(sa, wm * FM + i, 0);
-    __builtin_amdgcn_sched_barrier(0);
+    const char* na = a_ring + ((kt + 1) % NA) * A_BYTES;
+    const char* nb = b_ring + ((kt + 1) % NB) * B_BYTES;
 #if GEMM_SETPRIO
     __builtin_amdgcn_s_setprio(1);
 #endif
+    // First half: MFMAs on (a0, w0); this k-step's second-half fragments read.
 #pragma unroll
     for (int t = 0; t < NMF; ++t) {
       const int i = t / FN, j = t % FN;
       acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(w0[j], a0[i], acc[i][j], 0, 0, 0);
 #pragma unroll
-      for (int r = 0; r < NR1; ++r) {
-        if ((r * NMF) / NR1 == t) {
-          if (r < FN) w1[r] = frag(sb, wn * FN + r, 1);
-          else a1[r - FN] = frag(sa, wm * FM + (r - FN), 1);
-        }
-      }
-#pragma unroll
-      for (int d = 0; d < L1; ++d) {
-        if ((d * NMF) / L1 == t) {
-          if (B_FIRST) dma_b(kt_b, d);
-          else dma_a(kt_a, d);
-        }
-      }
+      for (int r = 0; r < NR; ++r)
+        if ((r * NMF) / NR == t) read_half(sa, sb, 1, r, a1, w1);
       __builtin_amdgcn_sched_barrier(0);
     }
+#if GEMM_SETPRIO
+    __builtin_amdgcn_s_setprio(0);
+#endif
+    __builtin_amdgcn_s_waitcnt(kWaitMid);
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+#if GEMM_SETPRIO
+    __builtin_amdgcn_s_setprio(1);
+#endif
+    // Second half: MFMAs on (a1, w1); the next k-step's first-half fragments
+    // read; this k-step's slots refilled (W first, then A).
 #pragma unroll
     for (int t = 0; t < NMF; ++t) {
       const int i = t / FN, j = t % FN;
       acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(w1[j], a1[i], acc[i][j], 0, 0, 0);
 #pragma unroll
-      for (int d = 0; d < L2; ++d) {
-        if ((d * NMF) / L2 == t) {
-          if (B_FIRST) dma_a(kt_a, d);
-          else dma_b(kt_b, d);
+      for (int r = 0; r < NR; ++r)
+        if ((r * NMF) / NR == t) read_half(na, nb, 0, r, a0, w0);
+#pragma unroll
+      for (int d = 0; d < ND; ++d) {
+        if ((d * NMF) / ND == t) {
+          if (d < B_LOADS) dma_b(kt + NB, d);
+          else dma_a(kt + NA, d - B_LOADS);
         }
       }
       __builtin_amdgcn_sched_barrier(0);
