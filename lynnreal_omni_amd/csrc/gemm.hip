@@ -43,6 +43,10 @@
 #ifndef GEMM_SETPRIO
 #define GEMM_SETPRIO 1
 #endif
+// Ping-pong k-loop for the 8-wave tiles (K % 128 == 0).
+#ifndef GEMM_PINGPONG
+#define GEMM_PINGPONG 1
+#endif
 // Rows of tiles per raster group of the XCD-aware tile order.
 #ifndef GEMM_GROUP_M
 #define GEMM_GROUP_M 8
@@ -233,24 +237,31 @@ __device__ __forceinline__ void store_tile_staged(const GemmArgs& p, const v4i (
                                                   int wn, int lane) {
   constexpr int PITCH = 2 * WN + 16;
   const int lr_ = lane & 15, lg = lane >> 4;
+  // Every scale and bias load of the wave is issued before the first is used
+  // (one memory round trip per tile, not one per column group), from clamped
+  // addresses so that no load sits under a branch.
   float rsv[FM];
+  float4 csv[FN];
+  uint2 bv[FN];
 #pragma unroll
   for (int i = 0; i < FM; ++i) {
     const int64_t row = m0 + wm * WM + 16 * i + lr_;
-    rsv[i] = row < p.m ? p.rs[row] : 0.0f;
+    rsv[i] = p.rs[row < p.m ? row : p.m - 1];
+  }
+#pragma unroll
+  for (int j = 0; j < FN; ++j) {
+    const int64_t col = n0 + wn * WN + 16 * j + 4 * lg;
+    const int64_t c = col < p.n ? col : p.n - 4;  // N % 8 == 0 on this path
+    csv[j] = *reinterpret_cast<const float4*>(p.cs + c);
+    if (BIAS) bv[j] = *reinterpret_cast<const uint2*>(p.bias + c);
   }
 #pragma unroll
   for (int j = 0; j < FN; ++j) {
     __builtin_amdgcn_sched_barrier(0);
-    const int64_t col = n0 + wn * WN + 16 * j + 4 * lg;
-    float4 cs = make_float4(0.f, 0.f, 0.f, 0.f);
+    const float4 cs = csv[j];
     float b0 = 0.f, b1 = 0.f, b2 = 0.f, b3 = 0.f;
-    if (col < p.n) {
-      cs = *reinterpret_cast<const float4*>(p.cs + col);
-      if (BIAS) {
-        const uint2 bb = *reinterpret_cast<const uint2*>(p.bias + col);
-        b0 = bf_lo(bb.x); b1 = bf_hi(bb.x); b2 = bf_lo(bb.y); b3 = bf_hi(bb.y);
-      }
+    if (BIAS) {
+      b0 = bf_lo(bv[j].x); b1 = bf_hi(bv[j].x); b2 = bf_lo(bv[j].y); b3 = bf_hi(bv[j].y);
     }
 #pragma unroll
     for (int i = 0; i < FM; ++i) {
@@ -418,7 +429,8 @@ __device__ __forceinline__ void dma16s(__amdgpu_buffer_rsrc_t rsrc, void* lds, u
 // +4 for the second k64 half) each group of 8 lanes then reads 8 distinct
 // 16-byte bank groups; measured on gfx950 this runs ds_read_b128 at 94% of
 // the rate of a contiguous read (an extra (R / 8) % 2 term drops it to 71%).
-template <int BM, int BN, int WAVES_M, int WAVES_N, int EPI, bool BIAS, int NA, int NB, bool KALIGNED>
+template <int BM, int BN, int WAVES_M, int WAVES_N, int EPI, bool BIAS, int NA, int NB, bool KALIGNED,
+          bool PP>
 __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_fast(GemmArgs p) {
   constexpr int BK = 128;
   constexpr int NWAVES = WAVES_M * WAVES_N;
@@ -518,6 +530,116 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_fast(GemmArgs p) 
 #pragma unroll
     for (int j = 0; j < FN; ++j) acc[i][j] = v4i{0, 0, 0, 0};
 
+  if constexpr (PP) {
+    // Ping-pong: waves 0-3 (one per SIMD) and waves 4-7 (the other wave of each
+    // SIMD) alternate between a compute phase (the 64 MFMAs of one k-step, from
+    // registers, no other instruction) and a memory phase (the 24 fragment reads
+    // of their next k-step, plus DMAs), one phase apart, with a barrier between
+    // phases. Each SIMD's MFMA pipe is then fed by one wave at a time that
+    // issues nothing else, while its partner's LDS reads and DMAs go to other
+    // units. Phase 2k: group 0 reads k-step k, group 1 computes k-step k - 1;
+    // phase 2k + 1: group 0 computes k-step k, group 1 reads it.
+    //
+    // A slot of k-step k is free once group 1 has read it (its lgkmcnt(0)
+    // before the barrier that ends phase 2k + 1). Group 0 refills the A ring
+    // (3 slots): A(k + 2) in its memory phase of k-step k, into the slot of
+    // k-step k - 1, and waits for A(k + 1) at the end of its compute phase of
+    // k-step k. Group 1 refills the W ring (2 slots): W(k + 2) into the slot it
+    // has just read, and waits for W(k + 1) before the barrier that ends its
+    // memory phase. Both waits land just before the barrier that ends phase
+    // 2k + 1, which publishes k-step k + 1 for group 0's read in phase 2k + 2.
+    static_assert(NWAVES == 8 && NA == 3 && NB == 2 && KALIGNED, "ping-pong layout");
+    constexpr int PA = BM / 8 / 4, PB = BN / 8 / 4;  // 1 KB DMAs per wave per k-step
+    static_assert(PA * 32 == BM && PB * 32 == BN && PA <= 15 && PB <= 15, "ping-pong DMA split");
+    const int grp = wave >> 2, q = wave & 3;
+    uint32_t pa_off[PA], pb_off[PB];
+#pragma unroll
+    for (int i = 0; i < PA; ++i) pa_off[i] = (uint32_t)(((q * PA + i) * 8 + drow) * K + dchunk);
+#pragma unroll
+    for (int j = 0; j < PB; ++j) pb_off[j] = (uint32_t)(((q * PB + j) * 8 + drow) * K + dchunk);
+    // DMAs past the last k-step re-read the last one (every address stays in
+    // the panel) into slots that no k-step reads again.
+    auto pdma_a = [&](int kt) {
+      const uint32_t soff = (uint32_t)((kt < KT ? kt : KT - 1) * BK);
+#pragma unroll
+      for (int i = 0; i < PA; ++i)
+        dma16s(ra, a_ring + (kt % NA) * A_BYTES + (q * PA + i) * 1024, pa_off[i], soff);
+    };
+    auto pdma_b = [&](int kt) {
+      const uint32_t soff = (uint32_t)((kt < KT ? kt : KT - 1) * BK);
+#pragma unroll
+      for (int j = 0; j < PB; ++j)
+        dma16s(rb, b_ring + (kt % NB) * B_BYTES + (q * PB + j) * 1024, pb_off[j], soff);
+    };
+    constexpr int kWaitA = 0x70 | 0xf00 | PA;  // vmcnt(PA): all but the newest k-step landed
+    constexpr int kWaitB = 0x70 | 0xf00 | PB;
+    constexpr int kWaitLds = 0xc07f;           // lgkmcnt(0)
+    v4i a0[FM], w0[FN], a1[FM], w1[FN];
+    auto read_all = [&](int kt) {
+      const char* sa = a_ring + (kt % NA) * A_BYTES;
+      const char* sb = b_ring + (kt % NB) * B_BYTES;
+#pragma unroll
+      for (int i = 0; i < FM; ++i) a0[i] = frag(sa, wm * FM + i, 0);
+#pragma unroll
+      for (int j = 0; j < FN; ++j) w0[j] = frag(sb, wn * FN + j, 0);
+#pragma unroll
+      for (int i = 0; i < FM; ++i) a1[i] = frag(sa, wm * FM + i, 1);
+#pragma unroll
+      for (int j = 0; j < FN; ++j) w1[j] = frag(sb, wn * FN + j, 1);
+    };
+    auto compute = [&]() {
+#pragma unroll
+      for (int t = 0; t < FM * FN; ++t) {
+        const int i = t / FN, j = t % FN;
+        acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(w0[j], a0[i], acc[i][j], 0, 0, 0);
+      }
+#pragma unroll
+      for (int t = 0; t < FM * FN; ++t) {
+        const int i = t / FN, j = t % FN;
+        acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(w1[j], a1[i], acc[i][j], 0, 0, 0);
+      }
+    };
+    // The MFMAs touch no memory: without the leading scheduling barrier the
+    // compiler would move the s_barrier above them.
+    auto barrier = [&]() {
+      __builtin_amdgcn_sched_barrier(0);
+      __builtin_amdgcn_s_barrier();
+      asm volatile("" ::: "memory");
+      __builtin_amdgcn_sched_barrier(0);
+    };
+    if (grp == 0) {
+      pdma_a(0);
+      pdma_a(1);
+      __builtin_amdgcn_s_waitcnt(kWaitA);
+      barrier();
+      for (int kt = 0; kt < KT; ++kt) {
+        read_all(kt);  // phase 2kt
+        pdma_a(kt + 2);
+        __builtin_amdgcn_s_waitcnt(kWaitLds);
+        barrier();
+        compute();  // phase 2kt + 1
+        __builtin_amdgcn_sched_barrier(0);  // the wait stays behind the MFMAs
+        __builtin_amdgcn_s_waitcnt(kWaitA);
+        barrier();
+      }
+      barrier();  // phase 2KT: group 1 computes the last k-step
+    } else {
+      pdma_b(0);
+      pdma_b(1);
+      __builtin_amdgcn_s_waitcnt(kWaitB);
+      barrier();
+      barrier();  // phase 0: group 0 reads k-step 0
+      for (int kt = 0; kt < KT; ++kt) {
+        read_all(kt);  // phase 2kt + 1
+        __builtin_amdgcn_s_waitcnt(kWaitLds);
+        pdma_b(kt + 2);
+        __builtin_amdgcn_s_waitcnt(kWaitB);
+        barrier();
+        compute();  // phase 2kt + 2
+        barrier();
+      }
+    }
+  } else {
   // One barrier per k-step, between its two halves. Fragments are always read
   // one half ahead: the second half's while the first half's MFMAs run, and the
   // next k-step's first half while the second half's MFMAs run, so no MFMA
@@ -615,6 +737,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_fast(GemmArgs p) 
     __builtin_amdgcn_s_setprio(0);
 #endif
   }
+  }
   // The trailing zero-fill DMAs must land before the workgroup's LDS is freed.
   __builtin_amdgcn_s_waitcnt(0x70 | 0xf00);  // vmcnt(0)
 
@@ -686,12 +809,13 @@ void launch_fast_cfg(GemmArgs& p, hipStream_t st) {
   p.tiles_m = (int)((p.m + BM - 1) / BM);
   p.tiles_n = (int)((p.n + BN - 1) / BN);
   const unsigned grid = (unsigned)(p.tiles_m * p.tiles_n);
+  constexpr bool kPingPong = GEMM_PINGPONG && WAVES_M * WAVES_N == 8 && NA == 3 && NB == 2;
   if (p.k % 128 == 0)
-    hipLaunchKernelGGL((gemm_fast<BM, BN, WAVES_M, WAVES_N, EPI, BIAS, NA, NB, true>), dim3(grid),
-                       dim3(64 * WAVES_M * WAVES_N), 0, st, p);
+    hipLaunchKernelGGL((gemm_fast<BM, BN, WAVES_M, WAVES_N, EPI, BIAS, NA, NB, true, kPingPong>),
+                       dim3(grid), dim3(64 * WAVES_M * WAVES_N), 0, st, p);
   else
-    hipLaunchKernelGGL((gemm_fast<BM, BN, WAVES_M, WAVES_N, EPI, BIAS, NA, NB, false>), dim3(grid),
-                       dim3(64 * WAVES_M * WAVES_N), 0, st, p);
+    hipLaunchKernelGGL((gemm_fast<BM, BN, WAVES_M, WAVES_N, EPI, BIAS, NA, NB, false, false>),
+                       dim3(grid), dim3(64 * WAVES_M * WAVES_N), 0, st, p);
 }
 
 template <int EPI, bool BIAS>
