@@ -47,6 +47,23 @@
 #ifndef GEMM_PINGPONG
 #define GEMM_PINGPONG 1
 #endif
+// Waves (along M) of the 256x80 tile.
+#ifndef GEMM_SKINNY_WAVES
+#define GEMM_SKINNY_WAVES 4
+#endif
+// Ring depths (A, W) of the weight-streaming tiles.
+#ifndef GEMM_SKINNY_NA
+#define GEMM_SKINNY_NA 4
+#endif
+#ifndef GEMM_SKINNY_NB
+#define GEMM_SKINNY_NB 3
+#endif
+#ifndef GEMM_SKINNY64_NA
+#define GEMM_SKINNY64_NA 4
+#endif
+#ifndef GEMM_SKINNY64_NB
+#define GEMM_SKINNY64_NB 12
+#endif
 // Rows of tiles per raster group of the XCD-aware tile order.
 #ifndef GEMM_GROUP_M
 #define GEMM_GROUP_M 8
@@ -277,11 +294,12 @@ __device__ __forceinline__ void store_tile_staged(const GemmArgs& p, const v4i (
   asm volatile("" ::: "memory");
   __builtin_amdgcn_sched_barrier(0);
 
-  constexpr int CPR = WN / 8;            // 16-byte chunks per row
-  constexpr int ITERS = WM * CPR / 64;   // rows of 16-byte chunks per lane
-  static_assert(WM * CPR % 64 == 0, "staging tile shape");
+  constexpr int CPR = WN / 8;                   // 16-byte chunks per row
+  constexpr int ITERS = (WM * CPR + 63) / 64;   // rows of 16-byte chunks per lane
+  constexpr bool kWhole = WM * CPR % 64 == 0;   // else the last pass is partial
+  static_assert(WN % 8 == 0, "staging tile shape");
   const bool seq_covers = p.sequence >= p.m;
-  if constexpr (EPI == EPI_GATED && WM <= 64 && ITERS % 4 == 0) {
+  if constexpr (EPI == EPI_GATED && WM <= 64 && kWhole && ITERS % 4 == 0) {
     // x + bf16(gate * y): the residual and gate chunks of 4 staging rows are
     // loaded before any of them is used, from clamped (always valid)
     // addresses, so the loads overlap instead of each waiting in turn (a load
@@ -330,6 +348,7 @@ __device__ __forceinline__ void store_tile_staged(const GemmArgs& p, const v4i (
 #pragma unroll 4
   for (int s = 0; s < ITERS; ++s) {
     const int q = s * 64 + lane;
+    if (!kWhole && q >= WM * CPR) break;
     const int r = q / CPR, ch = q % CPR;
     const int64_t row = m0 + wm * WM + r;
     const int64_t col = n0 + wn * WN + ch * 8;
@@ -437,12 +456,19 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_fast(GemmArgs p) 
   constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N;
   constexpr int FM = WM / 16, FN = WN / 16;
   constexpr int A_BYTES = BM * BK, B_BYTES = BN * BK;
-  constexpr int A_LOADS = BM / 8 / NWAVES, B_LOADS = BN / 8 / NWAVES;  // 1 KB DMAs per wave per k-step
+  // 1 KB DMA blocks (8 rows x 128 bytes) per k-step, and per wave. Every wave
+  // issues the same count (the wait counts assume it); where the blocks do not
+  // divide evenly, the surplus loads repeat the last block (same bytes to the
+  // same LDS place).
+  constexpr int A_BLOCKS = BM / 8, B_BLOCKS = BN / 8;
+  constexpr int A_LOADS = (A_BLOCKS + NWAVES - 1) / NWAVES, B_LOADS = (B_BLOCKS + NWAVES - 1) / NWAVES;
   // A k-steps live in a ring of NA LDS slots, W k-steps in a ring of NB: an
   // operand with d slots is fetched d - 1 k-steps ahead.
   static_assert(NWAVES == 4 || NWAVES == 8, "4 or 8 waves");
-  static_assert(A_LOADS * NWAVES * 8 == BM && B_LOADS * NWAVES * 8 == BN && A_LOADS >= 1 &&
-                    B_LOADS >= 1 && FM >= 1 && FN >= 1, "tile shape");
+  static_assert(BM % 16 == 0 && BN % 16 == 0 && FM * 16 * WAVES_M == BM && FN * 16 * WAVES_N == BN &&
+                    FM >= 1 && FN >= 1, "tile shape");
+  auto a_block = [](int w, int i) { return min(w * A_LOADS + i, A_BLOCKS - 1); };
+  auto b_block = [](int w, int j) { return min(w * B_LOADS + j, B_BLOCKS - 1); };
   // The operand rings, reused after the main loop as the epilogue's staging tiles.
   constexpr int RING_BYTES = NA * A_BYTES + NB * B_BYTES;
   constexpr int STAGING_BYTES = NWAVES * WM * (2 * WN + 16);
@@ -473,9 +499,9 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_fast(GemmArgs p) 
   const int dchunk = ((lane & 7) ^ drow) * 16;
   uint32_t a_off[A_LOADS], b_off[B_LOADS];
 #pragma unroll
-  for (int i = 0; i < A_LOADS; ++i) a_off[i] = (uint32_t)(((wave * A_LOADS + i) * 8 + drow) * K + dchunk);
+  for (int i = 0; i < A_LOADS; ++i) a_off[i] = (uint32_t)((a_block(wave, i) * 8 + drow) * K + dchunk);
 #pragma unroll
-  for (int j = 0; j < B_LOADS; ++j) b_off[j] = (uint32_t)(((wave * B_LOADS + j) * 8 + drow) * K + dchunk);
+  for (int j = 0; j < B_LOADS; ++j) b_off[j] = (uint32_t)((b_block(wave, j) * 8 + drow) * K + dchunk);
 
   // With K % 128 == 0 a DMA's per-lane offset is fixed and the k-step goes in
   // the scalar offset (no vector work per DMA). The rings keep issuing past the
@@ -487,22 +513,22 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_fast(GemmArgs p) 
   // past the last k-step every lane does.
   auto dma_a = [&](int kt, int i) {
     if constexpr (KALIGNED) {
-      dma16s(ra, a_ring + (kt % NA) * A_BYTES + (wave * A_LOADS + i) * 1024, a_off[i],
+      dma16s(ra, a_ring + (kt % NA) * A_BYTES + a_block(wave, i) * 1024, a_off[i],
              (uint32_t)((kt < KT ? kt : KT - 1) * BK));
       return;
     }
     const int64_t kbase = (int64_t)kt * BK;
-    dma16(ra, a_ring + (kt % NA) * A_BYTES + (wave * A_LOADS + i) * 1024,
+    dma16(ra, a_ring + (kt % NA) * A_BYTES + a_block(wave, i) * 1024,
           kbase + dchunk < K ? a_off[i] + (uint32_t)kbase : 0x80000000u);
   };
   auto dma_b = [&](int kt, int j) {
     if constexpr (KALIGNED) {
-      dma16s(rb, b_ring + (kt % NB) * B_BYTES + (wave * B_LOADS + j) * 1024, b_off[j],
+      dma16s(rb, b_ring + (kt % NB) * B_BYTES + b_block(wave, j) * 1024, b_off[j],
              (uint32_t)((kt < KT ? kt : KT - 1) * BK));
       return;
     }
     const int64_t kbase = (int64_t)kt * BK;
-    dma16(rb, b_ring + (kt % NB) * B_BYTES + (wave * B_LOADS + j) * 1024,
+    dma16(rb, b_ring + (kt % NB) * B_BYTES + b_block(wave, j) * 1024,
           kbase + dchunk < K ? b_off[j] + (uint32_t)kbase : 0x80000000u);
   };
   auto issue_a = [&](int kt) {
@@ -748,10 +774,11 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_fast(GemmArgs p) 
     __syncthreads();
     store_tile_staged<FM, FN, WM, WN, EPI, BIAS>(p, acc, smem + wave * WM * (2 * WN + 16), m0, n0,
                                                  wm, wn, lane);
-  } else if (EPI == EPI_RAW && p.nvec) {
+  } else if (EPI == EPI_RAW && FN % 2 == 0 && p.nvec) {
     __syncthreads();
-    store_tile_staged_raw<FM, FN, WM, WN>(p, acc, smem + wave * WM * (2 * WN + 16), m0, n0, wm, wn,
-                                          lane);
+    if constexpr (FN % 2 == 0)
+      store_tile_staged_raw<FM, FN, WM, WN>(p, acc, smem + wave * WM * (2 * WN + 16), m0, n0, wm,
+                                            wn, lane);
   } else {
     store_tile<FM, FN, WM, WN, EPI, BIAS>(p, acc, m0, n0, wm, wn, lane);
   }
@@ -836,6 +863,14 @@ void launch_fast(int tile, GemmArgs& p, hipStream_t st) {
     // 4 waves of 64x32 (24 KB k-steps), both operands GEMM_DEPTH_SMALL - 1
     // k-steps ahead: small-M GEMMs are bound by the DMA latency of their few
     // tiles, not by LDS or MFMA.
+    // Weight-streaming tiles for a few hundred rows: 4 waves of 64x80 (or
+    // 16x80). 256x80 makes one wave of tiles from N = 20480 at M <= 256, 64x80
+    // one wave from N = 5120 at M <= 256. They are bound by the latency of the
+    // DMA stream: 4 + 3 slots (158 KB) for 256x80 (A re-read from L2 by every
+    // CU dominates), and 4 + 12 (152 KB) for 64x80, whose weight ring holds 11
+    // k-steps in flight (A is L2-resident, W comes from HBM).
+    case LR_TILE_256x80: launch_fast_cfg<256, 80, GEMM_SKINNY_WAVES, 1, EPI, BIAS, GEMM_SKINNY_NA, GEMM_SKINNY_NB>(p, st); break;
+    case LR_TILE_64x80: launch_fast_cfg<64, 80, 4, 1, EPI, BIAS, GEMM_SKINNY64_NA, GEMM_SKINNY64_NB>(p, st); break;
     default: launch_fast_cfg<64, 128, 1, 4, EPI, BIAS, GEMM_DEPTH_SMALL, GEMM_DEPTH_SMALL>(p, st); break;
   }
 }
@@ -861,6 +896,7 @@ int tile_rows(int tile) {
   switch (tile) {
     case LR_TILE_256x256: case LR_TILE_256x256_W4x2: case LR_TILE_256x128: case LR_TILE_256x192:
       return 256;
+    case LR_TILE_256x80: return 256;
     case LR_TILE_128x256: case LR_TILE_128x128: return 128;
     default: return 64;
   }
@@ -869,6 +905,7 @@ int tile_cols(int tile) {
   switch (tile) {
     case LR_TILE_256x256: case LR_TILE_256x256_W4x2: case LR_TILE_128x256: return 256;
     case LR_TILE_256x192: return 192;
+    case LR_TILE_256x80: case LR_TILE_64x80: return 80;
     default: return 128;
   }
 }
@@ -884,6 +921,15 @@ int tile_cols(int tile) {
 int auto_tile(int64_t m, int64_t n) {
   const int64_t cus = 256;
   auto tiles = [&](int t) { return ((m + tile_rows(t) - 1) / tile_rows(t)) * ((n + tile_cols(t) - 1) / tile_cols(t)); };
+  // A few hundred rows (graph-replay timings at K = 5120): 64x80 when its
+  // tiles fit one wave (M = 256, N = 5120: 14.6 us against 16.2 us for
+  // 64x128; M = 64, N = 5120: 12.5 against 13.7), else 256x80 when N / 80
+  // tiles fit one wave (M = 200..256, N = 20480: 31-33 us against 35-39 us
+  // for 128x128). At M <= 128 with wide N the 64x128 tile stays ahead.
+  if (m <= 256) {
+    if (tiles(LR_TILE_64x80) <= (m > 128 ? cus : cus / 2)) return LR_TILE_64x80;
+    if (m > 128 && tiles(LR_TILE_256x80) <= cus) return LR_TILE_256x80;
+  }
   auto waves = [&](int t, int64_t slots) { return (tiles(t) + slots - 1) / slots; };
   const int64_t c256 = waves(LR_TILE_256x256_W4x2, cus) * 66;
   const int64_t c192 = waves(LR_TILE_256x192, cus) * 60;
@@ -908,7 +954,7 @@ extern "C" int lr_int8_gemm(const int8_t* a, const int8_t* b, int64_t b_stride_k
   LR_REQUIRE(m >= 0 && n >= 0 && k >= 0, "int8_gemm: negative shape");
   LR_REQUIRE(epilogue >= LR_EPI_BF16 && epilogue <= LR_EPI_RAW_INT32,
              "int8_gemm: unknown epilogue %d", epilogue);
-  LR_REQUIRE(tile >= LR_TILE_AUTO && tile <= LR_TILE_256x192, "int8_gemm: unknown tile %d",
+  LR_REQUIRE(tile >= LR_TILE_AUTO && tile <= LR_TILE_64x80, "int8_gemm: unknown tile %d",
              tile);
   if (m == 0 || n == 0) return LR_OK;
   LR_REQUIRE(a && b && c, "int8_gemm: null A/B/C");

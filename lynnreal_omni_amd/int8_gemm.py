@@ -29,6 +29,8 @@ _TILES = {
     (128, 128): _lib.TILE_128x128,
     (64, 128): _lib.TILE_64x128,
     (256, 192): _lib.TILE_256x192,
+    (256, 80): _lib.TILE_256x80,
+    (64, 80): _lib.TILE_64x80,
 }
 
 
