@@ -495,9 +495,12 @@ def run_c4(args):
 
 
 def _timed_launches(fn, iters, flush=None):
-    """Average us per call of `fn` between two HIP events on the current stream
-    (back-to-back calls). With `flush` (a 1 GiB buffer) the 256 MB MALL is
-    overwritten before every call and each call is timed alone: the median,
+    """Average us per call of `fn`, back to back: the calls are captured in a
+    HIP graph and the replay is timed between two HIP events, so kernels shorter
+    than the host's launch overhead are timed on the device (a callable that
+    cannot be captured, e.g. one that synchronizes with the host, is timed as
+    plain back-to-back launches). With `flush` (a 1 GiB buffer) the 256 MB MALL
+    is overwritten before every call and each call is timed alone: the median,
     with inputs cold in every cache."""
     import torch
     for _ in range(5):
@@ -505,6 +508,10 @@ def _timed_launches(fn, iters, flush=None):
     stream = torch.cuda.current_stream()
     torch.cuda.synchronize()
     if flush is None:
+        try:
+            return _event_time(fn, iters)
+        except RuntimeError:
+            torch.cuda.synchronize()
         start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         start.record(stream)
         for _ in range(iters):
