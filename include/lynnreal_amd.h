@@ -60,6 +60,7 @@ extern "C" {
 #define LR_TILE_256x192 8 /* 256x192 with a 4x2 wave grid (64x96 per wave) */
 #define LR_TILE_256x80 9 /* 256x80, 4 waves of 64x80: weight streaming for M <= 256 */
 #define LR_TILE_64x80 10 /* 64x80, 4 waves of 16x80: weight streaming for M <= 256 */
+#define LR_TILE_128x160 11 /* 128x160, 4 waves of 64x80: weight streaming for M <= 256 */
 
 /* Library version; bumped whenever a signature below changes. */
 int lr_abi_version(void);

@@ -871,6 +871,11 @@ void launch_fast(int tile, GemmArgs& p, hipStream_t st) {
     // k-steps in flight (A is L2-resident, W comes from HBM).
     case LR_TILE_256x80: launch_fast_cfg<256, 80, GEMM_SKINNY_WAVES, 1, EPI, BIAS, GEMM_SKINNY_NA, GEMM_SKINNY_NB>(p, st); break;
     case LR_TILE_64x80: launch_fast_cfg<64, 80, 4, 1, EPI, BIAS, GEMM_SKINNY64_NA, GEMM_SKINNY64_NB>(p, st); break;
+    // 4 waves of 64x80 over 128 rows: one wave of tiles from N = 20480 at
+    // M <= 256 that moves 36 KB per k-step against 44 KB for 256x80 (every CU
+    // re-reads its A rows from L2): 29 against 34 us at M = 256. 4 + 4 slots
+    // (144 KB).
+    case LR_TILE_128x160: launch_fast_cfg<128, 160, 2, 2, EPI, BIAS, 4, 4>(p, st); break;
     default: launch_fast_cfg<64, 128, 1, 4, EPI, BIAS, GEMM_DEPTH_SMALL, GEMM_DEPTH_SMALL>(p, st); break;
   }
 }
@@ -897,7 +902,7 @@ int tile_rows(int tile) {
     case LR_TILE_256x256: case LR_TILE_256x256_W4x2: case LR_TILE_256x128: case LR_TILE_256x192:
       return 256;
     case LR_TILE_256x80: return 256;
-    case LR_TILE_128x256: case LR_TILE_128x128: return 128;
+    case LR_TILE_128x256: case LR_TILE_128x128: case LR_TILE_128x160: return 128;
     default: return 64;
   }
 }
@@ -906,6 +911,7 @@ int tile_cols(int tile) {
     case LR_TILE_256x256: case LR_TILE_256x256_W4x2: case LR_TILE_128x256: return 256;
     case LR_TILE_256x192: return 192;
     case LR_TILE_256x80: case LR_TILE_64x80: return 80;
+    case LR_TILE_128x160: return 160;
     default: return 128;
   }
 }
@@ -923,12 +929,12 @@ int auto_tile(int64_t m, int64_t n) {
   auto tiles = [&](int t) { return ((m + tile_rows(t) - 1) / tile_rows(t)) * ((n + tile_cols(t) - 1) / tile_cols(t)); };
   // A few hundred rows (graph-replay timings at K = 5120): 64x80 when its
   // tiles fit one wave (M = 256, N = 5120: 14.6 us against 16.2 us for
-  // 64x128; M = 64, N = 5120: 12.5 against 13.7), else 256x80 when N / 80
-  // tiles fit one wave (M = 200..256, N = 20480: 31-33 us against 35-39 us
-  // for 128x128). At M <= 128 with wide N the 64x128 tile stays ahead.
+  // 64x128; M = 64, N = 5120: 12.5 against 13.7), else 128x160 when its tiles
+  // fit one wave (M = 256, N = 20480: 29 us against 34 us for 256x80 and
+  // 38 us for 128x128). At M <= 128 with wide N the 64x128 tile stays ahead.
   if (m <= 256) {
     if (tiles(LR_TILE_64x80) <= (m > 128 ? cus : cus / 2)) return LR_TILE_64x80;
-    if (m > 128 && tiles(LR_TILE_256x80) <= cus) return LR_TILE_256x80;
+    if (m > 128 && tiles(LR_TILE_128x160) <= cus) return LR_TILE_128x160;
   }
   auto waves = [&](int t, int64_t slots) { return (tiles(t) + slots - 1) / slots; };
   const int64_t c256 = waves(LR_TILE_256x256_W4x2, cus) * 66;
@@ -954,7 +960,7 @@ extern "C" int lr_int8_gemm(const int8_t* a, const int8_t* b, int64_t b_stride_k
   LR_REQUIRE(m >= 0 && n >= 0 && k >= 0, "int8_gemm: negative shape");
   LR_REQUIRE(epilogue >= LR_EPI_BF16 && epilogue <= LR_EPI_RAW_INT32,
              "int8_gemm: unknown epilogue %d", epilogue);
-  LR_REQUIRE(tile >= LR_TILE_AUTO && tile <= LR_TILE_64x80, "int8_gemm: unknown tile %d",
+  LR_REQUIRE(tile >= LR_TILE_AUTO && tile <= LR_TILE_128x160, "int8_gemm: unknown tile %d",
              tile);
   if (m == 0 || n == 0) return LR_OK;
   LR_REQUIRE(a && b && c, "int8_gemm: null A/B/C");

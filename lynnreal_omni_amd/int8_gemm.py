@@ -31,6 +31,7 @@ _TILES = {
     (256, 192): _lib.TILE_256x192,
     (256, 80): _lib.TILE_256x80,
     (64, 80): _lib.TILE_64x80,
+    (128, 160): _lib.TILE_128x160,
 }
 
 
