@@ -57,14 +57,15 @@ def parse():
     p.add_argument("--cpu-tokens", type=int, default=None,
                    help="tokens of the chain timed on the CPU (default: all of them, the whole config)")
     p.add_argument("--no-cpu-baseline", action="store_true")
-    p.add_argument("--workload", choices=("c3", "c1", "c4", "c5", "rows", "qk", "flash", "adaln"),
+    p.add_argument("--workload", choices=("c3", "c1", "c4", "c5", "rows", "qk", "flash", "adaln", "ceiling"),
                    default="c3",
                    help="c3: the projection chain (default, the headline line); c1: one W8A8 linear "
                         "(2048x5120 -> 5120) with the CPU torch path beside it; c4: the T=65536 W8A8 FFN "
                         "against the same shapes in bf16; c5: the chain at T=12288+317 with per-frame "
                         "modulation rows, and M=256 projections; rows: the HBM-bound row kernels at the "
                         "C2/C3 shape; qk: QK RMSNorm + RoPE; flash: Flash token selection; adaln: the "
-                        "adaLN table projection")
+                        "adaLN table projection; ceiling: the GEMM's MFMA stream alone, from registers "
+                        "(the power-limited INT8 ceiling, no memory traffic)")
     p.add_argument("--flush", action="store_true",
                    help="rows workload: overwrite the MALL before each launch and time launches one by one")
     p.add_argument("--no-vendor-gemm", dest="vendor_gemm", action="store_false",
@@ -688,6 +689,111 @@ def _cpu_name():
     return "unknown"
 
 
+CEILING_SOURCE = r"""
+// The GEMM's MFMA stream with no memory traffic: each wave holds 8 activation
+// and 16 weight fragments (bit patterns of real operands, read once) and 128
+// accumulators, and issues one k-step's 64 v_mfma_i32_16x16x64_i8 per
+// iteration in the GEMM's order, two waves per SIMD.
+#include <hip/hip_runtime.h>
+typedef int v4i __attribute__((ext_vector_type(4)));
+__global__ __launch_bounds__(512) void mfma_ceiling(const v4i* __restrict__ fa,
+                                                    const v4i* __restrict__ fw, int iters, int* out) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int set = (blockIdx.x * 8 + wave) % 64;
+  v4i a[8], w[16];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) a[i] = fa[(set * 8 + i) * 64 + lane];
+#pragma unroll
+  for (int j = 0; j < 16; ++j) w[j] = fw[(set * 16 + j) * 64 + lane];
+  v4i acc[4][8];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[i][j] = v4i{0, 0, 0, 0};
+  for (int it = 0; it < iters; ++it) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(w[8 * h + j], a[4 * h + i], acc[i][j], 0, 0, 0);
+  }
+  int s = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) s ^= acc[i][j].x ^ acc[i][j].y ^ acc[i][j].z ^ acc[i][j].w;
+  out[blockIdx.x * 512 + threadIdx.x] = s;
+}
+extern "C" int ceiling_launch(const void* fa, const void* fw, int iters, void* out, int blocks, void* stream) {
+  hipLaunchKernelGGL(mfma_ceiling, dim3(blocks), dim3(512), 0, (hipStream_t)stream, (const v4i*)fa,
+                     (const v4i*)fw, iters, (int*)out);
+  return (int)hipGetLastError();
+}
+"""
+
+
+def run_ceiling(args):
+    """The chip's INT8 MFMA rate with no memory traffic: the GEMM's k-step MFMA
+    stream (two waves per SIMD, 128 accumulators each) from registers, with the
+    operands' bit patterns taken from the bench's own quantized activations and
+    int8 weights, from all-zero operands and from uniform random int8. The probe
+    is compiled here with hipcc (it is not part of the library). Under the power
+    limit the clock follows the operands' bit activity; the GEMM's fraction of
+    this rate is the share its memory traffic leaves."""
+    import ctypes
+    import subprocess
+    import tempfile
+    import torch
+    work = tempfile.mkdtemp(prefix="lr_ceiling_")
+    src, lib = os.path.join(work, "ceiling.hip"), os.path.join(work, "libceiling.so")
+    with open(src, "w") as f:
+        f.write(CEILING_SOURCE)
+    subprocess.run(["hipcc", "--offload-arch=gfx950", "-O3", "-fPIC", "-shared", "-mllvm",
+                    "-amdgpu-mfma-vgpr-form", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+                    src, "-o", lib], check=True, capture_output=True)
+    probe = ctypes.CDLL(lib)
+    probe.ceiling_launch.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p,
+                                     ctypes.c_int, ctypes.c_void_p]
+    g = torch.Generator().manual_seed(20261201 + CONFIG_INDEX)
+    x = torch.randn(4096, 128, generator=g)
+    x[:, torch.randperm(128, generator=g)[:2]] *= 20
+    act = torch.clamp(torch.round(x / (x.abs().amax(1, keepdim=True) / 127)), -127, 127).to(torch.int8)
+    sources = {
+        "bench_operands": (act, torch.randint(-127, 128, (8192, 128), dtype=torch.int8, generator=g)),
+        "zeros": (torch.zeros(4096, 128, dtype=torch.int8), torch.zeros(8192, 128, dtype=torch.int8)),
+        "uniform_random": (torch.randint(-127, 128, (4096, 128), dtype=torch.int8, generator=g),
+                           torch.randint(-127, 128, (8192, 128), dtype=torch.int8, generator=g)),
+    }
+    blocks, iters = 1024, 400
+    out = torch.empty(blocks * 512, dtype=torch.int32, device="cuda")
+    ops = blocks * 8 * iters * 64 * 2 * 16 * 16 * 64
+    res = {}
+    for name, (a, w) in sources.items():
+        fa, fw = a.contiguous().cuda(), w.contiguous().cuda()   # 512 KB and 1 MB of fragments
+        launch = lambda: probe.ceiling_launch(fa.data_ptr(), fw.data_ptr(), iters, out.data_ptr(), blocks,
+                                             torch.cuda.current_stream().cuda_stream)
+        for _ in range(3):
+            assert launch() == 0
+        torch.cuda.synchronize()
+        times = []
+        for _ in range(max(args.steps, 5)):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            launch()
+            e1.record()
+            e1.synchronize()
+            times.append(e0.elapsed_time(e1) * 1e3)
+        us = statistics.median(times)
+        res[name] = {"us": round(us, 1), "tops": round(ops / (us * 1e-6) / 1e12, 1),
+                     "frac_peak": round(ops / (us * 1e-6) / 1e12 / PEAK_INT8_TOPS, 4)}
+    return _side_line("INT8 MFMA ceiling without memory traffic (TOPS)", res["bench_operands"]["tops"],
+                      "TOPS", args, "MFMA stream from registers (GEMM k-step order)", res, dtype="int8",
+                      config={"blocks": blocks, "waves_per_block": 8, "iterations": iters,
+                              "mfma": "v_mfma_i32_16x16x64_i8"})
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -707,7 +813,7 @@ def main():
         log(f"device {torch.cuda.get_device_name(0)}; C5 ragged chain and M=256 projections")
         print(json.dumps(run_c5(args)), flush=True)
         return 0
-    side = {"rows": run_rows, "qk": run_qk, "flash": run_flash, "adaln": run_adaln}
+    side = {"rows": run_rows, "qk": run_qk, "flash": run_flash, "adaln": run_adaln, "ceiling": run_ceiling}
     if args.workload in side:
         log(f"device {torch.cuda.get_device_name(0)}; workload {args.workload}")
         print(json.dumps(side[args.workload](args)), flush=True)
