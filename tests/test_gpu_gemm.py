@@ -129,16 +129,32 @@ def test_north_star_shape_whole_product():
     a = torch.randint(-127, 128, (m, k), dtype=torch.int8, generator=g).cuda()
     w = torch.randint(-127, 128, (n, k), dtype=torch.int8, generator=g).cuda()
     acc = int8_gemm.int8_matmul_int32(a, w.t())
-    assert torch.equal(acc, torch._int_mm(a, w.t()))
     rows = torch.cat([torch.arange(0, 64), torch.randint(64, m - 64, (64,), generator=g),
                       torch.arange(m - 64, m)])
     got = acc[rows.cuda()].cpu().numpy()
     expect = ref.int_mm(a[rows.cuda()].cpu().numpy(), w.cpu().numpy())
     assert np.array_equal(got, expect)
-    checksum_rows = acc.to(torch.int64).sum(dim=1).cpu()
-    # row sums by linearity: sum_n acc[m, n] = sum_k a[m, k] * (sum_n w[n, k])
-    expect_rows = (a.to(torch.int64) * w.to(torch.int64).sum(dim=0)).sum(dim=1).cpu()
-    assert torch.equal(checksum_rows, expect_rows)
+    a64, w64 = a.to(torch.int64), w.to(torch.int64)
+    # sums by linearity: sum_n acc[m, n] = sum_k a[m, k] * (sum_n w[n, k]) and
+    # sum_m acc[m, n] = sum_k (sum_m a[m, k]) * w[n, k]; a single wrong element
+    # changes both its row's and its column's sum
+    assert torch.equal(acc.to(torch.int64).sum(dim=1), (a64 * w64.sum(dim=0)).sum(dim=1))
+    assert torch.equal(acc.to(torch.int64).sum(dim=0), (w64 * a64.sum(dim=0)).sum(dim=1))
+    del a64, w64
+    again = int8_gemm.int8_matmul_int32(a, w.t())
+    assert torch.equal(acc, again), f"{int((acc != again).sum())} elements differ between two runs"
+    del again
+    other = torch._int_mm(a, w.t())
+    bad = (acc != other).nonzero()
+    if bad.numel():
+        pos = bad[:16].cpu()
+        exact = [int((a[r].to(torch.int64) * w[c].to(torch.int64)).sum()) for r, c in pos.tolist()]
+        ours = acc[pos[:, 0].cuda(), pos[:, 1].cuda()].cpu().tolist()
+        theirs = other[pos[:, 0].cuda(), pos[:, 1].cuda()].cpu().tolist()
+        detail = (f"{bad.shape[0]} elements differ from torch._int_mm; first (row, col, ours, "
+                  f"_int_mm, exact): {list(zip(pos.tolist(), ours, theirs, exact))}")
+        assert ours == exact, "kernel wrong: " + detail
+        assert theirs == exact, "torch._int_mm wrong: " + detail
 
 
 def test_torch_matmul_agrees_on_gpu():
