@@ -57,7 +57,8 @@ def parse():
     p.add_argument("--cpu-tokens", type=int, default=None,
                    help="tokens of the chain timed on the CPU (default: all of them, the whole config)")
     p.add_argument("--no-cpu-baseline", action="store_true")
-    p.add_argument("--workload", choices=("c3", "c1", "c4", "c5", "rows", "qk", "flash", "adaln", "ceiling"),
+    p.add_argument("--workload", choices=("c3", "c1", "c4", "c5", "rows", "qk", "flash", "adaln", "ceiling",
+                                          "shapes"),
                    default="c3",
                    help="c3: the projection chain (default, the headline line); c1: one W8A8 linear "
                         "(2048x5120 -> 5120) with the CPU torch path beside it; c4: the T=65536 W8A8 FFN "
@@ -65,7 +66,8 @@ def parse():
                         "modulation rows, and M=256 projections; rows: the HBM-bound row kernels at the "
                         "C2/C3 shape; qk: QK RMSNorm + RoPE; flash: Flash token selection; adaln: the "
                         "adaLN table projection; ceiling: the GEMM's MFMA stream alone, from registers "
-                        "(the power-limited INT8 ceiling, no memory traffic)")
+                        "(the power-limited INT8 ceiling, no memory traffic); shapes: the Flash "
+                        "model's four GEMM shapes at full M (D=5376), every large tile and hipBLASLt")
     p.add_argument("--flush", action="store_true",
                    help="rows workload: overwrite the MALL before each launch and time launches one by one")
     p.add_argument("--no-vendor-gemm", dest="vendor_gemm", action="store_false",
@@ -495,6 +497,53 @@ def run_c4(args):
     }
 
 
+def run_shapes(args):
+    """The Flash model's own GEMM shapes at full M, as the reference's install
+    check runs them (script/precompile.py:51-53): QKV 16385x21504x5376, out
+    16385x5376x7168, FFN-up 49153x28672x5376, FFN-down 16385x5376x14336, each a
+    bf16 product with row and column scales. Every shape is timed through the
+    automatic tile and through each large tile (so the automatic choice, whose
+    per-wave costs were set at K=5120, is checked at these K), with
+    torch._int_mm (hipBLASLt, int32 out) beside it."""
+    import torch
+    from lynnreal_omni_amd.int8_gemm import int8_matmul
+    shapes = {"qkv": (16385, 21504, 5376), "out": (16385, 5376, 7168),
+              "up": (49153, 28672, 5376), "down": (16385, 5376, 14336)}
+    tiles = [None, (256, 256), "256x256_w4x2", (256, 192), (256, 128), (128, 256), (128, 128)]
+    g = torch.Generator(device="cuda").manual_seed(219)
+    reps = max(args.steps // 4, 3)
+    kernels, total_ops, total_us = {}, 0, 0.0
+    for name, (m, n, k) in shapes.items():
+        a = torch.randint(-127, 128, (m, k), device="cuda", dtype=torch.int8, generator=g)
+        w = torch.randint(-127, 128, (n, k), device="cuda", dtype=torch.int8, generator=g).t()
+        rs = torch.rand(m, 1, device="cuda", generator=g) / 127
+        cs = torch.rand(1, n, device="cuda", generator=g) / 127
+        ops = 2 * m * n * k
+        per_tile = {}
+        for tile in tiles:
+            us = _event_time(lambda: int8_matmul(a, w, rs, cs, tile=tile), reps)
+            per_tile["auto" if tile is None else str(tile)] = round(us, 1)
+        auto_us = per_tile["auto"]
+        best = min(per_tile, key=per_tile.get)
+        vendor_us = _event_time(lambda: torch._int_mm(a, w), reps)
+        kernels[name] = {"m": m, "n": n, "k": k, "us": auto_us,
+                         "tops": round(ops / (auto_us * 1e-6) / 1e12, 1),
+                         "frac_peak": round(ops / (auto_us * 1e-6) / 1e12 / PEAK_INT8_TOPS, 4),
+                         "best_tile": best, "best_us": per_tile[best], "tiles_us": per_tile,
+                         "hipblaslt_int_mm_us": round(vendor_us, 1),
+                         "hipblaslt_tops": round(ops / (vendor_us * 1e-6) / 1e12, 1)}
+        log(name, json.dumps(kernels[name]))
+        total_ops += ops
+        total_us += auto_us
+        del a, w, rs, cs
+        torch.cuda.empty_cache()
+    return _side_line("Flash-model GEMM shapes at full M, INT8 TOPS (auto tile)",
+                      round(total_ops / (total_us * 1e-6) / 1e12, 1), "TOPS", args,
+                      "reference install-check shapes (script/precompile.py:51-53)", kernels,
+                      dtype="int8", pct_int8_peak=round(100 * total_ops / (total_us * 1e-6) / 1e12
+                                                        / PEAK_INT8_TOPS, 2))
+
+
 def _timed_launches(fn, iters, flush=None):
     """Average us per call of `fn`, back to back: the calls are captured in a
     HIP graph and the replay is timed between two HIP events, so kernels shorter
@@ -813,7 +862,8 @@ def main():
         log(f"device {torch.cuda.get_device_name(0)}; C5 ragged chain and M=256 projections")
         print(json.dumps(run_c5(args)), flush=True)
         return 0
-    side = {"rows": run_rows, "qk": run_qk, "flash": run_flash, "adaln": run_adaln, "ceiling": run_ceiling}
+    side = {"rows": run_rows, "qk": run_qk, "flash": run_flash, "adaln": run_adaln, "ceiling": run_ceiling,
+            "shapes": run_shapes}
     if args.workload in side:
         log(f"device {torch.cuda.get_device_name(0)}; workload {args.workload}")
         print(json.dumps(side[args.workload](args)), flush=True)

@@ -119,11 +119,45 @@ def test_reference_install_check_shapes(shape):
     assert hashlib.sha256(y.tobytes()).hexdigest() == want["y_sha256"]
 
 
+@pytest.mark.parametrize("m,n,k", [(16385, 21504, 5376), (16385, 5376, 7168),
+                                   (49153, 28672, 5376), (16385, 5376, 14336)], ids=str)
+def test_reference_full_m_install_shapes(m, n, k):
+    """The full-M shapes of the reference's install check (script/precompile.py:
+    51-53: the Flash model's QKV, out, FFN-up and FFN-down GEMMs with the
+    16385-row and 49153-row tails) with the check it makes there (:55-64): the
+    bf16 product equals the torch path's dequant of torch._int_mm, on the whole
+    output. The int32 accumulators also pass the row- and column-sum closed
+    forms, and sampled rows (both ends, so the one-row last tile) equal the C
+    oracle."""
+    from oracle import torch_path as tp
+    g = torch.Generator(device="cuda").manual_seed(219)
+    a = torch.randint(-127, 128, (m, k), device="cuda", dtype=torch.int8, generator=g)
+    w = torch.randint(-127, 128, (n, k), device="cuda", dtype=torch.int8, generator=g)
+    rs = torch.rand(m, 1, device="cuda", generator=g) / 127
+    cs = torch.rand(1, n, device="cuda", generator=g) / 127
+    acc = int8_gemm.int8_matmul_int32(a, w.t())
+    a64, w64 = a.to(torch.int64), w.to(torch.int64)
+    assert torch.equal(acc.to(torch.int64).sum(dim=1), (a64 * w64.sum(dim=0)).sum(dim=1))
+    assert torch.equal(acc.to(torch.int64).sum(dim=0), (w64 * a64.sum(dim=0)).sum(dim=1))
+    del a64, w64
+    assert torch.equal(acc, torch._int_mm(a, w.t()))
+    y = int8_gemm.int8_matmul(a, w.t(), rs, cs)
+    assert torch.equal(y, tp.epilogue(acc, rs, cs))
+    rows = torch.cat([torch.arange(0, 24), torch.randint(24, m - 24, (16,)), torch.arange(m - 24, m)])
+    a_rows = a[rows.cuda()].cpu().numpy()
+    w_np = w.cpu().numpy()
+    assert np.array_equal(acc[rows.cuda()].cpu().numpy(), ref.int_mm(a_rows, w_np))
+    expect = ref.linear(a_rows, rs[rows.cuda()].cpu().numpy(), w_np, cs.cpu().numpy())
+    assert np.array_equal(to_np(y[rows.cuda()]), expect)
+
+
 def test_north_star_shape_whole_product():
-    """M=12288, K=5120, N=20480: the whole int32 product equals torch._int_mm
-    on the GPU (hipBLASLt's INT8 GEMM, an independent implementation whose
-    results are exact integers), sampled rows equal the C oracle, and every
-    row sum equals its closed form by linearity."""
+    """M=12288, K=5120, N=20480: sampled rows equal the C oracle, every row
+    sum and column sum equals its closed form by linearity, a second run gives
+    the same output, and the whole int32 product equals torch._int_mm on the
+    GPU (hipBLASLt's INT8 GEMM, an independent implementation whose results are
+    exact integers); a difference from torch._int_mm is reported with the
+    exact products at the first differing elements."""
     g = gen(14)
     m, n, k = 12288, 20480, 5120
     a = torch.randint(-127, 128, (m, k), dtype=torch.int8, generator=g).cuda()
