@@ -570,10 +570,18 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_fast(GemmArgs p) 
     // before the barrier that ends phase 2k + 1). Group 0 refills the A ring
     // (3 slots): A(k + 2) in its memory phase of k-step k, into the slot of
     // k-step k - 1, and waits for A(k + 1) at the end of its compute phase of
-    // k-step k. Group 1 refills the W ring (2 slots): W(k + 2) into the slot it
-    // has just read, and waits for W(k + 1) before the barrier that ends its
+    // k-step k. Group 1 refills the W ring (2 slots) with W(k + 2), into the
+    // slot of k-step k, and waits for W(k + 1) before the barrier that ends its
     // memory phase. Both waits land just before the barrier that ends phase
     // 2k + 1, which publishes k-step k + 1 for group 0's read in phase 2k + 2.
+    // A wave's DMAs write the q-th quarter of the tile's W rows (q = wave % 4).
+    // With four waves across N (wn = q) no other wave of group 1 reads those
+    // rows, so the refill goes out as soon as the wave's own reads are done.
+    // With two waves across N each W row is read by two waves of group 1, and
+    // one wave's refill could overwrite rows the other is still reading (the
+    // per-wave lgkmcnt does not cover other waves): the refill then waits for
+    // the barrier that ends phase 2k + 1 and goes out at the start of group
+    // 1's compute phase.
     static_assert(NWAVES == 8 && NA == 3 && NB == 2 && KALIGNED, "ping-pong layout");
     constexpr int PA = BM / 8 / 4, PB = BN / 8 / 4;  // 1 KB DMAs per wave per k-step
     static_assert(PA * 32 == BM && PB * 32 == BN && PA <= 15 && PB <= 15, "ping-pong DMA split");
@@ -600,6 +608,8 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_fast(GemmArgs p) 
     constexpr int kWaitA = 0x70 | 0xf00 | PA;  // vmcnt(PA): all but the newest k-step landed
     constexpr int kWaitB = 0x70 | 0xf00 | PB;
     constexpr int kWaitLds = 0xc07f;           // lgkmcnt(0)
+    constexpr int kWaitLdsVm0 = 0x70;          // vmcnt(0) lgkmcnt(0)
+    constexpr bool kOwnW = WAVES_N == 4;       // wn == wave % 4 for every wave
     v4i a0[FM], w0[FN], a1[FM], w1[FN];
     auto read_all = [&](int kt) {
       const char* sa = a_ring + (kt % NA) * A_BYTES;
@@ -657,10 +667,21 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_fast(GemmArgs p) 
       barrier();  // phase 0: group 0 reads k-step 0
       for (int kt = 0; kt < KT; ++kt) {
         read_all(kt);  // phase 2kt + 1
-        __builtin_amdgcn_s_waitcnt(kWaitLds);
-        pdma_b(kt + 2);
-        __builtin_amdgcn_s_waitcnt(kWaitB);
-        barrier();
+        if constexpr (kOwnW) {
+          // This wave alone in its group reads the W rows it refills.
+          __builtin_amdgcn_s_waitcnt(kWaitLds);
+          pdma_b(kt + 2);
+          __builtin_amdgcn_s_waitcnt(kWaitB);  // W(kt + 1) landed
+          barrier();
+        } else {
+          // Other waves of this group may still be reading the rows this
+          // wave's DMAs would overwrite: refill after the barrier, by which
+          // every wave has read W(kt). W(kt + 1), issued one phase ago, is
+          // the only load in flight.
+          __builtin_amdgcn_s_waitcnt(kWaitLdsVm0);
+          barrier();
+          pdma_b(kt + 2);
+        }
         compute();  // phase 2kt + 2
         barrier();
       }
@@ -848,9 +869,12 @@ void launch_fast_cfg(GemmArgs& p, hipStream_t st) {
 template <int EPI, bool BIAS>
 void launch_fast(int tile, GemmArgs& p, hipStream_t st) {
   switch (tile) {
-    // 8 waves of 128x64; two 64 KB k-steps in LDS; 1 block per CU.
+    // 8 waves of 128x64; three A and two W 32 KB k-steps in LDS; 1 block per
+    // CU. The large shapes take it: with four waves across N each wave of the
+    // ping-pong loop refills only W rows that it alone reads in its group.
     case LR_TILE_256x256: launch_fast_cfg<256, 256, 2, 4, EPI, BIAS>(p, st); break;
-    // 8 waves of 64x128 (same block shape, other wave grid).
+    // 8 waves of 64x128 (same block shape, other wave grid; its W refill waits
+    // for a barrier, 3-4% slower at the FFN-up shape).
     case LR_TILE_256x256_W4x2: launch_fast_cfg<256, 256, 4, 2, EPI, BIAS>(p, st); break;
     // 8 waves of 64x96: 192-column tiles fill the CUs where 256-column ones leave a
     // partial wave (N = 5120 at M = 2048: 216 tiles instead of 160).
@@ -937,12 +961,12 @@ int auto_tile(int64_t m, int64_t n) {
     if (m > 128 && tiles(LR_TILE_128x160) <= cus) return LR_TILE_128x160;
   }
   auto waves = [&](int t, int64_t slots) { return (tiles(t) + slots - 1) / slots; };
-  const int64_t c256 = waves(LR_TILE_256x256_W4x2, cus) * 66;
+  const int64_t c256 = waves(LR_TILE_256x256, cus) * 66;
   const int64_t c192 = waves(LR_TILE_256x192, cus) * 60;
   const int64_t c128 = waves(LR_TILE_128x128, 2 * cus) * 36;
   const int64_t c64 = waves(LR_TILE_64x128, cus) * 18;
   if (c192 < c256 && c192 < c128 && c192 < c64) return LR_TILE_256x192;
-  if (c256 <= c128 && c256 <= c64) return LR_TILE_256x256_W4x2;
+  if (c256 <= c128 && c256 <= c64) return LR_TILE_256x256;
   return c128 <= c64 ? LR_TILE_128x128 : LR_TILE_64x128;
 }
 

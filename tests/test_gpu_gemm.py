@@ -191,6 +191,32 @@ def test_north_star_shape_whole_product():
         assert theirs == exact, "torch._int_mm wrong: " + detail
 
 
+@pytest.mark.parametrize("tile", [None, (256, 256), "256x256_w4x2"], ids=str)
+def test_north_star_shape_repeats_identically(tile):
+    """The same launch repeated ten times back to back on one stream gives the
+    same bytes every time, int32 and bf16 + GELU (integer accumulation has one
+    answer, so any difference is a race in the kernel's LDS or DMA schedule);
+    the first run's int32 row sums equal their closed form."""
+    g = torch.Generator(device="cuda").manual_seed(23)
+    m, n, k = 12288, 20480, 5120
+    a = torch.randint(-127, 128, (m, k), device="cuda", dtype=torch.int8, generator=g)
+    w = torch.randint(-127, 128, (n, k), device="cuda", dtype=torch.int8, generator=g)
+    rs = torch.rand(m, device="cuda", generator=g) / 127 / 40
+    cs = torch.rand(n, device="cuda", generator=g) / 127
+    bias = (0.02 * torch.randn(n, device="cuda", generator=g)).bfloat16()
+    first = int8_gemm.int8_matmul_int32(a, w.t(), tile=tile)
+    expect_rows = (a.to(torch.int64) * w.to(torch.int64).sum(dim=0)).sum(dim=1)
+    assert torch.equal(first.to(torch.int64).sum(dim=1), expect_rows)
+    for rep in range(9):
+        again = int8_gemm.int8_matmul_int32(a, w.t(), tile=tile)
+        assert torch.equal(first, again), f"repeat {rep + 1}: {int((first != again).sum())} int32 differ"
+    del again
+    y0 = int8_gemm.int8_matmul(a, w.t(), rs, cs, bias, tile=tile, activation="gelu_tanh")
+    for rep in range(9):
+        y = int8_gemm.int8_matmul(a, w.t(), rs, cs, bias, tile=tile, activation="gelu_tanh")
+        assert torch.equal(y0, y), f"repeat {rep + 1}: {int((y0 != y).sum())} bf16 differ"
+
+
 def test_torch_matmul_agrees_on_gpu():
     """_torch_matmul (torch._int_mm on the GPU) and the MFMA kernel agree
     bit for bit, as the reference's install check demands."""
