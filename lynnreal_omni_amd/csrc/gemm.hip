@@ -299,17 +299,22 @@ __device__ __forceinline__ void store_tile_staged(const GemmArgs& p, const v4i (
   constexpr bool kWhole = WM * CPR % 64 == 0;   // else the last pass is partial
   static_assert(WN % 8 == 0, "staging tile shape");
   const bool seq_covers = p.sequence >= p.m;
-  if constexpr (EPI == EPI_GATED && WM <= 64 && kWhole && ITERS % 4 == 0) {
+  if constexpr (EPI == EPI_GATED && WM <= 128 && kWhole && ITERS % 4 == 0) {
     // x + bf16(gate * y): the residual and gate chunks of 4 staging rows are
     // loaded before any of them is used, from clamped (always valid)
     // addresses, so the loads overlap instead of each waiting in turn (a load
     // under a branch, or after a store the compiler cannot prove disjoint,
     // would serialise them). The table row of each of the wave's WM rows is
-    // read once, by lane r, and fetched per chunk with ds_bpermute. The
-    // residual is read once (non-temporal loads); the gate rows are shared.
-    const int64_t my_row = m0 + wm * WM + (lane < WM ? lane : 0);
-    const int tr_lane = (int)clamp_index(
-        p.indices[my_row < p.m ? (seq_covers ? my_row : my_row % p.sequence) : 0], p.table_rows);
+    // read once, by lane r % 64 (rows 64.. into a second register), and
+    // fetched per chunk with ds_bpermute. The residual is read once
+    // (non-temporal loads); the gate rows are shared.
+    auto table_row_of = [&](int r) {
+      const int64_t row = m0 + wm * WM + (r < WM ? r : 0);
+      return (int)clamp_index(
+          p.indices[row < p.m ? (seq_covers ? row : row % p.sequence) : 0], p.table_rows);
+    };
+    const int tr_lane = table_row_of(lane);
+    const int tr_lane_hi = WM > 64 ? table_row_of(64 + lane) : 0;
     constexpr int BATCH = 4;
 #pragma unroll 1
     for (int s0 = 0; s0 < ITERS; s0 += BATCH) {
@@ -325,7 +330,9 @@ __device__ __forceinline__ void store_tile_staged(const GemmArgs& p, const v4i (
         ok[b] = row < p.m && col < p.n;
         const int64_t row_l = ok[b] ? row : m0, col_l = ok[b] ? col : n0;
         o[b] = row * p.n + col;
-        const int tr = __builtin_amdgcn_ds_bpermute(4 * r, tr_lane);
+        const int tr_lo = __builtin_amdgcn_ds_bpermute(4 * r, tr_lane);
+        const int tr = WM > 64 ? (r < 64 ? tr_lo : __builtin_amdgcn_ds_bpermute(4 * (r - 64), tr_lane_hi))
+                               : tr_lo;
         xv[b] = load_nt(reinterpret_cast<const uint4*>(p.resid + row_l * p.n + col_l));
         gv[b] = *reinterpret_cast<const uint4*>(p.table + (int64_t)tr * p.table_width +
                                                  (int64_t)p.gate_slot * p.n + col_l);
