@@ -217,6 +217,27 @@ def test_north_star_shape_repeats_identically(tile):
         assert torch.equal(y0, y), f"repeat {rep + 1}: {int((y0 != y).sum())} bf16 differ"
 
 
+@pytest.mark.parametrize("tile", TILES, ids=str)
+def test_every_tile_repeats_identically(tile):
+    """Every tile, C1's shape (M=2048, K=5120, N=5120): ten back-to-back
+    launches give the same int32 and bf16 + GELU bytes, and the int32 result
+    equals torch._int_mm."""
+    g = torch.Generator(device="cuda").manual_seed(29)
+    m, n, k = 2048, 5120, 5120
+    a = torch.randint(-127, 128, (m, k), device="cuda", dtype=torch.int8, generator=g)
+    w = torch.randint(-127, 128, (n, k), device="cuda", dtype=torch.int8, generator=g)
+    rs = torch.rand(m, device="cuda", generator=g) / 127 / 40
+    cs = torch.rand(n, device="cuda", generator=g) / 127
+    bias = (0.02 * torch.randn(n, device="cuda", generator=g)).bfloat16()
+    first = int8_gemm.int8_matmul_int32(a, w.t(), tile=tile)
+    assert torch.equal(first, torch._int_mm(a, w.t()))
+    y0 = int8_gemm.int8_matmul(a, w.t(), rs, cs, bias, tile=tile, activation="gelu_tanh")
+    for rep in range(9):
+        assert torch.equal(first, int8_gemm.int8_matmul_int32(a, w.t(), tile=tile)), f"int32 repeat {rep + 1}"
+        y = int8_gemm.int8_matmul(a, w.t(), rs, cs, bias, tile=tile, activation="gelu_tanh")
+        assert torch.equal(y0, y), f"repeat {rep + 1}: {int((y0 != y).sum())} bf16 differ"
+
+
 def test_torch_matmul_agrees_on_gpu():
     """_torch_matmul (torch._int_mm on the GPU) and the MFMA kernel agree
     bit for bit, as the reference's install check demands."""
