@@ -59,10 +59,10 @@
 #define GEMM_SKINNY_NB 3
 #endif
 #ifndef GEMM_SKINNY64_NA
-#define GEMM_SKINNY64_NA 4
+#define GEMM_SKINNY64_NA 8
 #endif
 #ifndef GEMM_SKINNY64_NB
-#define GEMM_SKINNY64_NB 12
+#define GEMM_SKINNY64_NB 8
 #endif
 // Rows of tiles per raster group of the XCD-aware tile order.
 #ifndef GEMM_GROUP_M
@@ -898,8 +898,11 @@ void launch_fast(int tile, GemmArgs& p, hipStream_t st) {
     // 16x80). 256x80 makes one wave of tiles from N = 20480 at M <= 256, 64x80
     // one wave from N = 5120 at M <= 256. They are bound by the latency of the
     // DMA stream: 4 + 3 slots (158 KB) for 256x80 (A re-read from L2 by every
-    // CU dominates), and 4 + 12 (152 KB) for 64x80, whose weight ring holds 11
-    // k-steps in flight (A is L2-resident, W comes from HBM).
+    // CU dominates), and 8 + 8 (144 KB) for 64x80, both rings 7 k-steps ahead
+    // (A is L2-resident, W comes from HBM). Graph-replayed at N = K = 5120:
+    // 14.5-14.9 us at M = 256 against 15.3-15.6 for 4 + 12, and 11.8-12.2
+    // against 12.6-12.7 at M = 64; splits such as 6 + 10, 9 + 7 and 10 + 6
+    // measured about 20% slower than either.
     case LR_TILE_256x80: launch_fast_cfg<256, 80, GEMM_SKINNY_WAVES, 1, EPI, BIAS, GEMM_SKINNY_NA, GEMM_SKINNY_NB>(p, st); break;
     case LR_TILE_64x80: launch_fast_cfg<64, 80, 4, 1, EPI, BIAS, GEMM_SKINNY64_NA, GEMM_SKINNY64_NB>(p, st); break;
     // 4 waves of 64x80 over 128 rows: one wave of tiles from N = 20480 at
