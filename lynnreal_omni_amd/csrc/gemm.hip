@@ -910,6 +910,12 @@ void launch_fast(int tile, GemmArgs& p, hipStream_t st) {
     // re-reads its A rows from L2): 29 against 34 us at M = 256. 4 + 4 slots
     // (144 KB).
     case LR_TILE_128x160: launch_fast_cfg<128, 160, 2, 2, EPI, BIAS, 4, 4>(p, st); break;
+    // 8 waves of 96x64 (the 2x4 grid, so the early W refill): where 256x256
+    // tiles leave the last wave a quarter empty (M = 12288, N = 5120: 960
+    // tiles = 3.75 waves) its 1280 tiles make 5 full waves. Each tile carries
+    // more fixed cost per op, so it pays only at long K: FFN-down (K = 20480)
+    // 865 against 881 us, out-proj (K = 5120) 231 against 224 us.
+    case LR_TILE_192x256: launch_fast_cfg<192, 256, 2, 4, EPI, BIAS>(p, st); break;
     default: launch_fast_cfg<64, 128, 1, 4, EPI, BIAS, GEMM_DEPTH_SMALL, GEMM_DEPTH_SMALL>(p, st); break;
   }
 }
@@ -936,13 +942,15 @@ int tile_rows(int tile) {
     case LR_TILE_256x256: case LR_TILE_256x256_W4x2: case LR_TILE_256x128: case LR_TILE_256x192:
       return 256;
     case LR_TILE_256x80: return 256;
+    case LR_TILE_192x256: return 192;
     case LR_TILE_128x256: case LR_TILE_128x128: case LR_TILE_128x160: return 128;
     default: return 64;
   }
 }
 int tile_cols(int tile) {
   switch (tile) {
-    case LR_TILE_256x256: case LR_TILE_256x256_W4x2: case LR_TILE_128x256: return 256;
+    case LR_TILE_256x256: case LR_TILE_256x256_W4x2: case LR_TILE_128x256: case LR_TILE_192x256:
+      return 256;
     case LR_TILE_256x192: return 192;
     case LR_TILE_256x80: case LR_TILE_64x80: return 80;
     case LR_TILE_128x160: return 160;
@@ -958,7 +966,7 @@ int tile_cols(int tile) {
 // shape with the fewest wave-microseconds wins, ties to the larger tile
 // (256x192 only when strictly better: M = 2048, N = 5120 runs 216 of its
 // tiles in one wave, 60 us against 67 us for 160 tiles of 256x256).
-int auto_tile(int64_t m, int64_t n) {
+int auto_tile(int64_t m, int64_t n, int64_t k) {
   const int64_t cus = 256;
   auto tiles = [&](int t) { return ((m + tile_rows(t) - 1) / tile_rows(t)) * ((n + tile_cols(t) - 1) / tile_cols(t)); };
   // A few hundred rows (graph-replay timings at K = 5120): 64x80 when its
@@ -976,7 +984,14 @@ int auto_tile(int64_t m, int64_t n) {
   const int64_t c128 = waves(LR_TILE_128x128, 2 * cus) * 36;
   const int64_t c64 = waves(LR_TILE_64x128, cus) * 18;
   if (c192 < c256 && c192 < c128 && c192 < c64) return LR_TILE_256x192;
-  if (c256 <= c128 && c256 <= c64) return LR_TILE_256x256;
+  if (c256 <= c128 && c256 <= c64) {
+    // 192x256 against 256x256 by per-tile time a + b*K (us, fitted at K = 5120
+    // and 20480 on M = 12288, N = 5120): a longer K spreads 192x256's larger
+    // fixed cost per op and leaves the wave count to decide.
+    const double t256 = (double)waves(LR_TILE_256x256, cus) * (1.3 + 0.01068 * (double)k);
+    const double t192 = (double)waves(LR_TILE_192x256, cus) * (3.9 + 0.008255 * (double)k);
+    return t192 < 0.99 * t256 ? LR_TILE_192x256 : LR_TILE_256x256;
+  }
   return c128 <= c64 ? LR_TILE_128x128 : LR_TILE_64x128;
 }
 
@@ -994,7 +1009,7 @@ extern "C" int lr_int8_gemm(const int8_t* a, const int8_t* b, int64_t b_stride_k
   LR_REQUIRE(m >= 0 && n >= 0 && k >= 0, "int8_gemm: negative shape");
   LR_REQUIRE(epilogue >= LR_EPI_BF16 && epilogue <= LR_EPI_RAW_INT32,
              "int8_gemm: unknown epilogue %d", epilogue);
-  LR_REQUIRE(tile >= LR_TILE_AUTO && tile <= LR_TILE_128x160, "int8_gemm: unknown tile %d",
+  LR_REQUIRE(tile >= LR_TILE_AUTO && tile <= LR_TILE_192x256, "int8_gemm: unknown tile %d",
              tile);
   if (m == 0 || n == 0) return LR_OK;
   LR_REQUIRE(a && b && c, "int8_gemm: null A/B/C");
@@ -1032,7 +1047,7 @@ extern "C" int lr_int8_gemm(const int8_t* a, const int8_t* b, int64_t b_stride_k
   if (!fast) {
     LR_REQUIRE((m + 63) / 64 <= 65535, "int8_gemm: generic path supports M <= 4194240");
   } else {
-    if (tile == LR_TILE_AUTO) tile = auto_tile(m, n);
+    if (tile == LR_TILE_AUTO) tile = auto_tile(m, n, k);
     const int64_t tiles = ((m + tile_rows(tile) - 1) / tile_rows(tile)) *
                           ((n + tile_cols(tile) - 1) / tile_cols(tile));
     LR_REQUIRE(tiles <= 0x7fffffffLL, "int8_gemm: too many tiles");

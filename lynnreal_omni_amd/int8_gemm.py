@@ -32,6 +32,7 @@ _TILES = {
     (256, 80): _lib.TILE_256x80,
     (64, 80): _lib.TILE_64x80,
     (128, 160): _lib.TILE_128x160,
+    (192, 256): _lib.TILE_192x256,
 }
 
 
