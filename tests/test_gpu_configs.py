@@ -65,23 +65,37 @@ def test_c1_linear_whole_output_bit_exact():
 
 
 @torch.inference_mode()
+@pytest.mark.parametrize("tile", [None, (128, 160), (64, 80), (256, 80)], ids=str)
 @pytest.mark.parametrize("n", [5120, 20480])
 @pytest.mark.parametrize("m", [256, 200, 64, 1])
-def test_skinny_projection_whole_output_bit_exact(m, n):
+def test_skinny_projection_whole_output_bit_exact(m, n, tile):
     """BASELINE config 5's decode-like projections (M = 256, K = 5120, N = 5120
-    and 20480) and smaller M through the auto tile: int32 accumulators and the
-    bf16 epilogue over the whole output."""
-    g = torch.Generator().manual_seed(20261201 + 4 + m + n)
-    k = 5120
-    x = bf16_randn((m, k), g, outliers=0.01)
-    w, s, b = _weights(g, n, k)
-    q, qs = tp.quantize(x)
+    and 20480) and smaller M, through the auto tile and each small-M tile:
+    int32 accumulators and the bf16 epilogue over the whole output."""
+    q, qs, w, s, b, want_acc, want_y = _skinny_case(m, n)
     wd = w.cuda()
-    acc = int8_matmul_int32(q.cuda(), wd.t())
-    want_acc = tp.int_mm(q, w)
+    acc = int8_matmul_int32(q.cuda(), wd.t(), tile=tile)
     assert torch.equal(acc.cpu(), want_acc)
-    y = int8_matmul(q.cuda(), wd.t(), qs.cuda(), s.cuda(), b.cuda())
-    assert torch.equal(y.cpu(), tp.epilogue(want_acc, qs, s.reshape(1, -1), b))
+    y = int8_matmul(q.cuda(), wd.t(), qs.cuda(), s.cuda(), b.cuda(), tile=tile)
+    assert torch.equal(y.cpu(), want_y)
+
+
+_SKINNY = {}
+
+
+def _skinny_case(m, n):
+    """Inputs and CPU-oracle outputs of one skinny shape, computed once per
+    shape for all the tiles that are checked against them."""
+    if (m, n) not in _SKINNY:
+        g = torch.Generator().manual_seed(20261201 + 4 + m + n)
+        k = 5120
+        x = bf16_randn((m, k), g, outliers=0.01)
+        w, s, b = _weights(g, n, k)
+        q, qs = tp.quantize(x)
+        want_acc = tp.int_mm(q, w)
+        _SKINNY.clear()
+        _SKINNY[(m, n)] = (q, qs, w, s, b, want_acc, tp.epilogue(want_acc, qs, s.reshape(1, -1), b))
+    return _SKINNY[(m, n)]
 
 
 def _c5_inputs(g, video=12288, text=317, ffn=20480, up=None):
