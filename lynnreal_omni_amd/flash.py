@@ -87,7 +87,7 @@ def _on_grid(coordinate: torch.Tensor, alphabet: torch.Tensor, stride: int) -> t
     """Whether each coordinate (a member of the sorted `alphabet` of distinct
     values) is every stride-th distinct value counting from the smallest, or
     the largest one: its rank in the alphabet decides."""
-    rank = torch.searchsorted(alphabet, coordinate)
+    rank = torch.searchsorted(alphabet, coordinate.contiguous())
     return (rank % stride == 0) | (rank == alphabet.numel() - 1)
 
 
