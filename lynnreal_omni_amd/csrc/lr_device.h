@@ -243,17 +243,20 @@ __device__ __forceinline__ float fast_gelu_tanh(float x) {
 // lane l ^ o. 32 and 16 use the gfx950 permlane swaps, whose two results hold
 // (v[l ^ o], v[l]) in some order, so only their sum or max is formed; 8 is a
 // rotation by 8 within a 16-lane row; 4 is a half-row mirror (l -> 7 - l)
-// followed by a quad reversal; 2 and 1 are quad permutations.
+// followed by a quad reversal; 2 and 1 are quad permutations. Every source
+// lane of these patterns exists, so bound_ctrl changes no value; it is set
+// because it lets the compiler fold the move into the add, max or multiply
+// that uses it (one v_add_f32_dpp instead of a v_mov_b32_dpp and a v_add_f32).
 template <int O>
 __device__ __forceinline__ float xor_partner(float v) {
   const int u = __float_as_int(v);
-  if (O == 8) return __int_as_float(__builtin_amdgcn_mov_dpp(u, 0x128, 0xf, 0xf, false));
+  if (O == 8) return __int_as_float(__builtin_amdgcn_mov_dpp(u, 0x128, 0xf, 0xf, true));
   if (O == 4) {
-    const int m = __builtin_amdgcn_mov_dpp(u, 0x141, 0xf, 0xf, false);
-    return __int_as_float(__builtin_amdgcn_mov_dpp(m, 0x1b, 0xf, 0xf, false));
+    const int m = __builtin_amdgcn_mov_dpp(u, 0x141, 0xf, 0xf, true);
+    return __int_as_float(__builtin_amdgcn_mov_dpp(m, 0x1b, 0xf, 0xf, true));
   }
-  if (O == 2) return __int_as_float(__builtin_amdgcn_mov_dpp(u, 0x4e, 0xf, 0xf, false));
-  return __int_as_float(__builtin_amdgcn_mov_dpp(u, 0xb1, 0xf, 0xf, false));
+  if (O == 2) return __int_as_float(__builtin_amdgcn_mov_dpp(u, 0x4e, 0xf, 0xf, true));
+  return __int_as_float(__builtin_amdgcn_mov_dpp(u, 0xb1, 0xf, 0xf, true));
 }
 
 template <bool MAX>

@@ -51,8 +51,13 @@ __device__ __forceinline__ uint4 normalize8(const uint4& x, const uint4& w, floa
   return pack8(xf);
 }
 
-__device__ __forceinline__ float rsqrt_row(float eps, int64_t head_dim, float s) {
-  const float ms = s / (float)head_dim + eps;
+// head_dim = 8L is a power of two, so s / head_dim is exactly s * (1 / head_dim)
+// (both are the correctly rounded s * 2^-k); the multiply avoids the
+// correctly rounded division's ten-instruction expansion.
+template <int L>
+__device__ __forceinline__ float rsqrt_row(float eps, float s) {
+  static_assert((L & (L - 1)) == 0, "power-of-two head_dim");
+  const float ms = s * (1.0f / (float)(8 * L)) + eps;
   return 1.0f / __builtin_sqrtf(ms);
 }
 
@@ -140,8 +145,12 @@ __global__ __launch_bounds__(256) void qk_norm_rope(QkArgs p) {
     const float4 c0 = cr[0], c1 = cr[1], s0 = sr[0], s1 = sr[1];
     c[0] = c0.x; c[1] = c0.y; c[2] = c0.z; c[3] = c0.w; c[4] = c1.x; c[5] = c1.y; c[6] = c1.z; c[7] = c1.w;
     sn[0] = s0.x; sn[1] = s0.y; sn[2] = s0.z; sn[3] = s0.w; sn[4] = s1.x; sn[5] = s1.y; sn[6] = s1.z; sn[7] = s1.w;
+    // The first half's out = a - bf16(p * s) is a + bf16(p * -s) exactly
+    // (negation is exact and round-to-nearest-even is symmetric), so the sign
+    // goes into sin once per token and the loop always adds.
+    const bool first = j < D;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) c[e] = round_bf(c[e]), sn[e] = round_bf(sn[e]);
+    for (int e = 0; e < 8; ++e) c[e] = round_bf(c[e]), sn[e] = first ? -round_bf(sn[e]) : round_bf(sn[e]);
   }
   // Byte offsets inside the token (the descriptors end at head `heads`).
   const uint32_t q_step = (uint32_t)(2 * RPW * p.q_hs), k_step = (uint32_t)(2 * RPW * p.k_hs);
@@ -156,8 +165,8 @@ __global__ __launch_bounds__(256) void qk_norm_rope(QkArgs p) {
     // The next group (zeros past the last head).
     const uint4 qn_x = buf_load16(rq, q_off), kn_x = buf_load16(rk, k_off);
     // Every lane takes part in the cross-lane steps; heads past the end hold zeros.
-    const float q_rstd = rsqrt_row(p.eps, p.head_dim, sumsq8<L>(qx));
-    const float k_rstd = rsqrt_row(p.eps, p.head_dim, sumsq8<L>(kx));
+    const float q_rstd = rsqrt_row<L>(p.eps, sumsq8<L>(qx));
+    const float k_rstd = rsqrt_row<L>(p.eps, sumsq8<L>(kx));
     uint4 qn, kn;
     if (D == 0) {
       qn = normalize8(qx, qw, q_rstd);
@@ -168,16 +177,14 @@ __global__ __launch_bounds__(256) void qk_norm_rope(QkArgs p) {
       float nq[8], nk[8], pq[8], pk[8];
       normalize8f(qx, qw, q_rstd, nq);
       normalize8f(kx, kw, k_rstd, nk);
-      const bool left = j < D;  // first half of the rotary dims: out = a - b
+      const bool left = j < D;  // first half of the rotary dims: the partner is chunk j + D
       partner8<D>(nq, pq, left);
       partner8<D>(nk, pk, left);
       if (j < 2 * D) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-          const float aq = round_bf(nq[e] * c[e]), bq = round_bf(pq[e] * sn[e]);
-          const float ak = round_bf(nk[e] * c[e]), bk = round_bf(pk[e] * sn[e]);
-          nq[e] = left ? aq - bq : aq + bq;
-          nk[e] = left ? ak - bk : ak + bk;
+          nq[e] = round_bf(nq[e] * c[e]) + round_bf(pq[e] * sn[e]);
+          nk[e] = round_bf(nk[e] * c[e]) + round_bf(pk[e] * sn[e]);
         }
       }
       qn = pack8(nq);
