@@ -64,6 +64,14 @@
 #ifndef GEMM_SKINNY64_NB
 #define GEMM_SKINNY64_NB 8
 #endif
+// Staging rows whose residual and gate chunks the gated epilogue loads
+// before using any of them, where it divides the wave's rows of chunks (else
+// 4). Chain timings: 6 took FFN-down's 192x256 tiles (12 rows) from 900 to
+// 896-897 us; 8 spills registers in the 256x256 tile (out-proj 281 -> 342 us)
+// and 12 in the 192x256 one (900 -> 1416 us).
+#ifndef GEMM_GATED_BATCH
+#define GEMM_GATED_BATCH 6
+#endif
 // Rows of tiles per raster group of the XCD-aware tile order.
 #ifndef GEMM_GROUP_M
 #define GEMM_GROUP_M 8
@@ -315,7 +323,7 @@ __device__ __forceinline__ void store_tile_staged(const GemmArgs& p, const v4i (
     };
     const int tr_lane = table_row_of(lane);
     const int tr_lane_hi = WM > 64 ? table_row_of(64 + lane) : 0;
-    constexpr int BATCH = 4;
+    constexpr int BATCH = ITERS % GEMM_GATED_BATCH == 0 ? GEMM_GATED_BATCH : 4;
 #pragma unroll 1
     for (int s0 = 0; s0 < ITERS; s0 += BATCH) {
       uint4 xv[BATCH], gv[BATCH], v[BATCH];
