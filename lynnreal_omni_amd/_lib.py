@@ -25,7 +25,8 @@ LIBRARY = pathlib.Path(__file__).resolve().parent / "liblynnreal_amd.so"
 LR_OK, LR_EINVAL, LR_EUNSUPPORTED, LR_EHIP, LR_ENOMEM = 0, 1, 2, 3, 4
 EPI_BF16, EPI_GELU_TANH, EPI_GATED_RESIDUAL, EPI_RAW_INT32 = 0, 1, 2, 3
 (TILE_AUTO, TILE_256x256, TILE_256x128, TILE_128x256, TILE_128x128, TILE_64x128, TILE_GENERIC,
- TILE_256x256_W4x2, TILE_256x192, TILE_256x80, TILE_64x80, TILE_128x160, TILE_192x256) = range(13)
+ TILE_256x256_W4x2, TILE_256x192, TILE_256x80, TILE_64x80, TILE_128x160, TILE_192x256,
+ TILE_256x256_PERSISTENT) = range(14)
 ABI_VERSION = 1
 
 _P = ctypes.c_void_p

@@ -145,8 +145,10 @@ __device__ __forceinline__ void store_scalar(const GemmArgs& p, int64_t row, int
 }
 
 // ----------------------------------------------------------- tile order ----
-__device__ __forceinline__ void tile_coords(const GemmArgs& p, int& tm, int& tn) {
-  const int pid = blockIdx.x;
+// pid is the tile's position in launch order; the hardware deals workgroups
+// to the 8 XCDs round-robin, so pid % 8 is the XCD (for a persistent grid
+// too, whose size is a multiple of 8).
+__device__ __forceinline__ void tile_coords(const GemmArgs& p, int pid, int& tm, int& tn) {
   const int total = p.tiles_m * p.tiles_n;
   const int xcd = pid & 7, local = pid >> 3;
   const int q = total >> 3, r = total & 7;
@@ -463,8 +465,13 @@ __device__ __forceinline__ void dma16s(__amdgpu_buffer_rsrc_t rsrc, void* lds, u
 // +4 for the second k64 half) each group of 8 lanes then reads 8 distinct
 // 16-byte bank groups; measured on gfx950 this runs ds_read_b128 at 94% of
 // the rate of a contiguous read (an extra (R / 8) % 2 term drops it to 71%).
+//
+// PERSIST: a grid of at most one workgroup per CU loops over the tiles in
+// launch order (pid = blockIdx.x, + gridDim.x, ...), the schedule of the
+// reference's persistent kernel (model/int8_tma.py:12-29); otherwise each
+// workgroup computes one tile.
 template <int BM, int BN, int WAVES_M, int WAVES_N, int EPI, bool BIAS, int NA, int NB, bool KALIGNED,
-          bool PP>
+          bool PP, bool PERSIST = false>
 __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_fast(GemmArgs p) {
   constexpr int BK = 128;
   constexpr int NWAVES = WAVES_M * WAVES_N;
@@ -492,8 +499,10 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_fast(GemmArgs p) 
   char* const a_ring = smem;
   char* const b_ring = smem + NA * A_BYTES;
 
+  const int tiles = p.tiles_m * p.tiles_n;
+  for (int pid = blockIdx.x;;) {
   int tm, tn;
-  tile_coords(p, tm, tn);
+  tile_coords(p, pid, tm, tn);
   const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
   // Wave-uniform, so that everything derived from it (LDS addresses, M0) stays scalar.
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
@@ -818,6 +827,13 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_fast(GemmArgs p) 
   } else {
     store_tile<FM, FN, WM, WN, EPI, BIAS>(p, acc, m0, n0, wm, wn, lane);
   }
+  if constexpr (!PERSIST) break;
+  pid += gridDim.x;
+  if (pid >= tiles) break;
+  // Every wave is done with this tile's staging area before the next tile's
+  // DMAs refill the rings that share its LDS.
+  __syncthreads();
+  }
 }
 
 // -------------------------------------------------------- generic GEMM ----
@@ -881,9 +897,28 @@ void launch_fast_cfg(GemmArgs& p, hipStream_t st) {
                        dim3(grid), dim3(64 * WAVES_M * WAVES_N), 0, st, p);
 }
 
+// The persistent 256x256 block (K % 128 == 0, else one tile per workgroup):
+// one workgroup per CU, rounded down to a multiple of the 8 XCDs.
+template <int EPI, bool BIAS>
+void launch_persistent(GemmArgs& p, hipStream_t st) {
+  if (p.k % 128 != 0) {
+    launch_fast_cfg<256, 256, 2, 4, EPI, BIAS>(p, st);
+    return;
+  }
+  p.tiles_m = (int)((p.m + 255) / 256);
+  p.tiles_n = (int)((p.n + 255) / 256);
+  const int64_t tiles = (int64_t)p.tiles_m * p.tiles_n;
+  const int64_t cus = compute_units() >= 8 ? compute_units() / 8 * 8 : 8;
+  const unsigned grid = (unsigned)(tiles < cus ? tiles : cus);
+  hipLaunchKernelGGL((gemm_fast<256, 256, 2, 4, EPI, BIAS, GEMM_RING_A, GEMM_RING_B, true,
+                                GEMM_PINGPONG && GEMM_RING_A == 3 && GEMM_RING_B == 2, true>),
+                     dim3(grid), dim3(512), 0, st, p);
+}
+
 template <int EPI, bool BIAS>
 void launch_fast(int tile, GemmArgs& p, hipStream_t st) {
   switch (tile) {
+    case LR_TILE_256x256_PERSISTENT: launch_persistent<EPI, BIAS>(p, st); break;
     // 8 waves of 128x64; three A and two W 32 KB k-steps in LDS; 1 block per
     // CU. The large shapes take it: with four waves across N each wave of the
     // ping-pong loop refills only W rows that it alone reads in its group.
@@ -948,6 +983,7 @@ void dispatch_bias(bool generic, int tile, bool bias, GemmArgs& p, hipStream_t s
 int tile_rows(int tile) {
   switch (tile) {
     case LR_TILE_256x256: case LR_TILE_256x256_W4x2: case LR_TILE_256x128: case LR_TILE_256x192:
+    case LR_TILE_256x256_PERSISTENT:
       return 256;
     case LR_TILE_256x80: return 256;
     case LR_TILE_192x256: return 192;
@@ -958,6 +994,7 @@ int tile_rows(int tile) {
 int tile_cols(int tile) {
   switch (tile) {
     case LR_TILE_256x256: case LR_TILE_256x256_W4x2: case LR_TILE_128x256: case LR_TILE_192x256:
+    case LR_TILE_256x256_PERSISTENT:
       return 256;
     case LR_TILE_256x192: return 192;
     case LR_TILE_256x80: case LR_TILE_64x80: return 80;
@@ -1017,7 +1054,7 @@ extern "C" int lr_int8_gemm(const int8_t* a, const int8_t* b, int64_t b_stride_k
   LR_REQUIRE(m >= 0 && n >= 0 && k >= 0, "int8_gemm: negative shape");
   LR_REQUIRE(epilogue >= LR_EPI_BF16 && epilogue <= LR_EPI_RAW_INT32,
              "int8_gemm: unknown epilogue %d", epilogue);
-  LR_REQUIRE(tile >= LR_TILE_AUTO && tile <= LR_TILE_192x256, "int8_gemm: unknown tile %d",
+  LR_REQUIRE(tile >= LR_TILE_AUTO && tile <= LR_TILE_256x256_PERSISTENT, "int8_gemm: unknown tile %d",
              tile);
   if (m == 0 || n == 0) return LR_OK;
   LR_REQUIRE(a && b && c, "int8_gemm: null A/B/C");

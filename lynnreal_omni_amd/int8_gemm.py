@@ -40,7 +40,8 @@ def _tile_id(tile) -> int:
     if tile is None:
         return _lib.TILE_AUTO
     if isinstance(tile, str):
-        named = {"generic": _lib.TILE_GENERIC, "256x256_w4x2": _lib.TILE_256x256_W4x2}
+        named = {"generic": _lib.TILE_GENERIC, "256x256_w4x2": _lib.TILE_256x256_W4x2,
+                 "persistent": _lib.TILE_256x256_PERSISTENT}
         if tile in named:
             return named[tile]
         raise ValueError(f"unknown tile {tile!r}")

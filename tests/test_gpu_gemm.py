@@ -20,6 +20,7 @@ from oracle import reference as ref
 pytestmark = pytest.mark.gpu
 
 TILES = [None, (256, 256), "256x256_w4x2", (256, 192), (256, 80), (64, 80), (128, 160), (192, 256), (256, 128), (128, 256), (128, 128), (64, 128),
+         "persistent",
          "generic"]
 
 
@@ -293,12 +294,14 @@ def test_c4_shapes_beyond_2gib():
     assert np.array_equal(acc[rows_d].cpu().numpy(), ref.int_mm(want_q, w_dn.cpu().numpy()))
 
 
-def test_int8_tma_entry_matches_int8_matmul():
-    """model/int8_tma.py:33-41's entry point: same output as int8_matmul, and
-    the reference's tile tuples map onto HIP tiles."""
+@pytest.mark.parametrize("m,n,k", [(1024, 768, 1024), (16385, 5376, 7168), (20000, 2560, 384)])
+def test_int8_tma_entry_matches_int8_matmul(m, n, k):
+    """model/int8_tma.py:33-41's entry point (the persistent GEMM): same output
+    as int8_matmul, and the reference's tile tuples map onto HIP tiles. The
+    long-M shapes (the reference's M >= 16384 regime) give each of the 256
+    workgroups 3-6 tiles, with M and N tails."""
     from lynnreal_omni_amd import int8_tma
-    g = gen(16)
-    m, n, k = 1024, 768, 1024
+    g = gen(16 + m)
     a = torch.randint(-127, 128, (m, k), dtype=torch.int8, generator=g).cuda()
     w = torch.randint(-127, 128, (n, k), dtype=torch.int8, generator=g).cuda()
     rs = (torch.rand(m, 1, generator=g) / 127).cuda()
@@ -307,9 +310,10 @@ def test_int8_tma_entry_matches_int8_matmul():
     y = int8_tma.matmul(a, w.t(), rs, cs, bias)
     assert torch.equal(y, int8_gemm.int8_matmul(a, w.t(), rs, cs, bias))
     assert torch.equal(int8_tma.matmul(a, w.t(), rs, cs, bias, tile=(128, 128, 128, 8, 3)), y)
-    want = ref.dequant(ref.int_mm(a.cpu().numpy(), w.cpu().numpy()), rs.cpu().numpy(), cs.cpu().numpy(),
-                       to_np(bias))
-    assert np.array_equal(to_np(y), want)
+    rows = np.unique(np.r_[0, 1, 255, 256, m // 2, m - 257, m - 256, m - 1])
+    want = ref.dequant(ref.int_mm(a[rows].cpu().numpy(), w.cpu().numpy()), rs[rows].cpu().numpy(),
+                       cs.cpu().numpy(), to_np(bias))
+    assert np.array_equal(to_np(y[rows]), want)
 
 
 @pytest.mark.parametrize("act", [None, "gelu_tanh", "swiglu"])

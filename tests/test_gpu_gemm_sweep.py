@@ -16,6 +16,7 @@ from oracle import reference as ref
 pytestmark = pytest.mark.gpu
 
 TILES = [None, (256, 256), "256x256_w4x2", (256, 192), (256, 80), (64, 80), (128, 160), (192, 256), (256, 128), (128, 256), (128, 128), (64, 128),
+         "persistent",
          "generic"]
 EPILOGUES = ["int32", "bf16", "gelu_tanh", "gated"]
 
