@@ -5,6 +5,8 @@ validation (model/int8_gemm.py:97-98, model/int8.py:29-30), tile mapping,
 Int8Linear's buffers and torch backend (model/int8.py:6-68), the converter
 (model/int8.py:71-104) and the error classifier (model/acceleration.py:49-56).
 """
+import pathlib
+import re
 import types
 
 import numpy as np
@@ -13,7 +15,7 @@ import torch
 from torch import nn
 
 from helpers import bf16_randn, to_np
-from lynnreal_omni_amd import acceleration, int8_gemm, kernels
+from lynnreal_omni_amd import _lib, acceleration, int8_gemm, int8_tma, kernels
 from lynnreal_omni_amd.int8 import Int8Linear, quantize_transformer, quantize_weight
 from oracle import reference as ref
 
@@ -32,6 +34,33 @@ def test_tile_mapping():
     for bad in ((32, 32, 64, 4, 2), (512, 512, 1, 1, 1), "fast", (1,)):
         with pytest.raises(ValueError):
             int8_gemm._tile_id(bad)
+
+
+def test_tile_ids_match_the_header():
+    """Every LR_TILE_* of the C header has the same value in the Python
+    bindings, and the named tiles map onto them."""
+    header = pathlib.Path(__file__).resolve().parents[1] / "include" / "lynnreal_amd.h"
+    ids = {m.group(1): int(m.group(2)) for m in re.finditer(r"#define LR_TILE_(\w+) (\d+)", header.read_text())}
+    assert len(ids) >= 14
+    for name, value in ids.items():
+        assert getattr(_lib, "TILE_" + name) == value, name
+    assert int8_gemm._tile_id("persistent") == ids["256x256_PERSISTENT"]
+    assert int8_gemm._tile_id("256x256_w4x2") == ids["256x256_W4x2"]
+    assert int8_gemm._tile_id((192, 256, 128, 8, 3)) == ids["192x256"]
+
+
+def test_int8_tma_default_tile_is_the_persistent_gemm(monkeypatch):
+    """model/int8_tma.py:33-41's default tile runs the persistent GEMM; any
+    other tile tuple is passed on to int8_matmul's tile mapping."""
+    seen = []
+    monkeypatch.setattr(int8_tma, "int8_matmul", lambda *args, **kw: seen.append(kw["tile"]))
+    a = torch.zeros(4, 8, dtype=torch.int8)
+    b = torch.zeros(3, 8, dtype=torch.int8).t()
+    int8_tma.matmul(a, b, None, None)
+    int8_tma.matmul(a, b, None, None, tile=(128, 128, 128, 8, 3))
+    assert seen == ["persistent", (128, 128, 128, 8, 3)]
+    with pytest.raises(ValueError, match="TMA requires"):
+        int8_tma.matmul(a, b.contiguous(), None, None)
 
 
 def test_int8_matmul_validation():
