@@ -105,6 +105,31 @@ int lr_int8_gemm(const int8_t* a, const int8_t* b, int64_t b_stride_k, int64_t b
                  int64_t table_rows, int64_t table_width, const int64_t* indices,
                  int64_t sequence, int gate_slot, int tile, void* stream);
 
+/* lr_int8_gemm with a caller-provided device workspace for split-K: the
+ * K dimension is divided over `splits` workgroups per output tile, which
+ * write int32 partial sums to the workspace; a second kernel adds them (exact
+ * integer sums) and applies the same epilogue, so the outputs equal
+ * lr_int8_gemm's bit for bit. splits: 0 = chosen by shape (split only where
+ * the tiles would leave CUs idle), 1 = none, 2..64 = forced (K % 128 == 0,
+ * splits <= K / 128, N % 4 == 0). The library never allocates: workspace is
+ * device memory of workspace_bytes >= lr_int8_gemm_workspace_size (256-byte
+ * aligned), used only by the call's kernels on `stream`, so calls that share
+ * one workspace must be ordered on one stream. With workspace NULL no split
+ * is taken unless forced (then LR_EINVAL). Replaces the same reference
+ * functions as lr_int8_gemm (model/int8_gemm.py:96-163, :13-46), whose Triton
+ * autotuner covers small M with small tiles (model/int8_gemm.py:49-52). */
+int lr_int8_gemm_ws(const int8_t* a, const int8_t* b, int64_t b_stride_k, int64_t b_stride_n,
+                    int64_t m, int64_t n, int64_t k, const float* row_scale, const float* col_scale,
+                    const void* bias, void* c, int epilogue, const void* residual, const void* table,
+                    int64_t table_rows, int64_t table_width, const int64_t* indices,
+                    int64_t sequence, int gate_slot, void* workspace, int64_t workspace_bytes,
+                    int splits, int tile, void* stream);
+
+/* Workspace bytes lr_int8_gemm_ws needs for this shape, splits and tile
+ * (0 when its schedule does not split K). Sizing helper of lr_int8_gemm_ws;
+ * the reference has no counterpart (its Triton GEMM keeps no partials). */
+int64_t lr_int8_gemm_workspace_size(int64_t m, int64_t n, int64_t k, int splits, int tile);
+
 /* Stand-alone INT32 -> bf16 dequant epilogue.
  * Replaces model/kernels.py:41-46 (int8_epilogue):
  *   out[m,n] = bf16(((float)acc[m,n] * a_scale[m]) * w_scale[n] + bias[n]).

@@ -39,6 +39,8 @@ SIGNATURES = {
     "lr_quantize_rows": [_P, _I64, _I64, _P, _P, _P],
     "lr_int8_gemm": [_P, _P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _I32, _P, _P, _I64,
                      _I64, _P, _I64, _I32, _I32, _P],
+    "lr_int8_gemm_ws": [_P, _P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _I32, _P, _P, _I64,
+                        _I64, _P, _I64, _I32, _P, _I64, _I32, _I32, _P],
     "lr_int8_epilogue": [_P, _P, _P, _P, _P, _I64, _I64, _P],
     "lr_rms_adaln": [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I32, _I32, _F32, _P],
     "lr_rms_adaln_quant": [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I32, _I32,
@@ -87,6 +89,8 @@ def load() -> ctypes.CDLL:
             fn.restype = ctypes.c_int
         lib.lr_last_error.argtypes = []
         lib.lr_last_error.restype = ctypes.c_char_p
+        lib.lr_int8_gemm_workspace_size.argtypes = [_I64, _I64, _I64, _I32, _I32]
+        lib.lr_int8_gemm_workspace_size.restype = ctypes.c_int64
         if lib.lr_abi_version() != ABI_VERSION:
             raise RuntimeError(f"{path} has ABI {lib.lr_abi_version()}, expected {ABI_VERSION}")
         _lib = lib
@@ -143,3 +147,23 @@ def stream(t: torch.Tensor) -> int:
 
 def ptr(t: torch.Tensor | None) -> int | None:
     return None if t is None else t.data_ptr()
+
+
+_workspaces: dict[tuple[int, int], torch.Tensor] = {}
+
+
+def workspace(t: torch.Tensor, nbytes: int) -> tuple[int | None, int]:
+    """(pointer, bytes) of a device workspace of at least `nbytes` for the
+    caller's current stream on t's device, or (None, 0) when none is needed.
+
+    One buffer is kept per (device, stream) and grown on demand: kernels that
+    share it run in stream order, and torch's caching allocator reuses a
+    replaced buffer only behind the work already queued on that stream."""
+    if nbytes <= 0:
+        return None, 0
+    key = (t.device.index if t.device.index is not None else torch.cuda.current_device(), stream(t))
+    buf = _workspaces.get(key)
+    if buf is None or buf.numel() < nbytes:
+        buf = torch.empty(nbytes, dtype=torch.uint8, device=t.device)
+        _workspaces[key] = buf
+    return buf.data_ptr(), buf.numel()

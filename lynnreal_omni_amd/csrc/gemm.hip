@@ -95,6 +95,7 @@ struct GemmArgs {
   int64_t table_rows, table_width, sequence;
   int gate_slot;
   int tiles_m, tiles_n, group_m;
+  int splits;  // split-K: workgroups per tile along K (1: none); their int32 partials go to c
   int nvec;    // N % 4 == 0 and C/bias/col_scale/residual aligned for 4-wide access
   int staged;  // nvec, N % 8 == 0 and 16-byte aligned C/residual/table rows: whole-line stores
 };
@@ -470,6 +471,12 @@ __device__ __forceinline__ void dma16s(__amdgpu_buffer_rsrc_t rsrc, void* lds, u
 // launch order (pid = blockIdx.x, + gridDim.x, ...), the schedule of the
 // reference's persistent kernel (model/int8_tma.py:12-29); otherwise each
 // workgroup computes one tile.
+//
+// Split-K (p.splits = S > 1, one tile per workgroup, raw int32 epilogue):
+// workgroup g computes k-steps [s * KT / S, (s + 1) * KT / S) of tile g / S,
+// s = g % S, and writes those partial sums to slice s of
+// p.c (int32 [S, M, N]); splitk_reduce adds the slices (exact integer sums,
+// so any split gives the same int32 result) and applies the epilogue.
 template <int BM, int BN, int WAVES_M, int WAVES_N, int EPI, bool BIAS, int NA, int NB, bool KALIGNED,
           bool PP, bool PERSIST = false>
 __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_fast(GemmArgs p) {
@@ -500,7 +507,13 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_fast(GemmArgs p) 
   char* const b_ring = smem + NA * A_BYTES;
 
   const int tiles = p.tiles_m * p.tiles_n;
-  for (int pid = blockIdx.x;;) {
+  const int kt_all = (int)((p.k + BK - 1) / BK);
+  const int splits = PERSIST ? 1 : p.splits;
+  const int slice = PERSIST ? 0 : (int)blockIdx.x % splits;
+  // k-steps [kbase, kend) of the tile; no slice is empty when splits <= KT.
+  const int kbase = slice * kt_all / splits, kend = (slice + 1) * kt_all / splits;
+  if (!PERSIST && p.splits > 1) p.c = static_cast<int32_t*>(p.c) + (int64_t)slice * p.m * p.n;
+  for (int pid = PERSIST ? (int)blockIdx.x : (int)blockIdx.x / p.splits;;) {
   int tm, tn;
   tile_coords(p, pid, tm, tn);
   const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
@@ -508,7 +521,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_fast(GemmArgs p) 
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int wm = wave / WAVES_N, wn = wave % WAVES_N;
   const int64_t K = p.k;
-  const int KT = (int)((K + BK - 1) / BK);
+  const int KT = kend - kbase;
 
   const int64_t rows_a = min((int64_t)BM, p.m - m0);
   const int64_t rows_b = min((int64_t)BN, p.n - n0);
@@ -538,22 +551,22 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_fast(GemmArgs p) 
   auto dma_a = [&](int kt, int i) {
     if constexpr (KALIGNED) {
       dma16s(ra, a_ring + (kt % NA) * A_BYTES + a_block(wave, i) * 1024, a_off[i],
-             (uint32_t)((kt < KT ? kt : KT - 1) * BK));
+             (uint32_t)((kbase + (kt < KT ? kt : KT - 1)) * BK));
       return;
     }
-    const int64_t kbase = (int64_t)kt * BK;
+    const int64_t kbyte = (int64_t)(kbase + kt) * BK;
     dma16(ra, a_ring + (kt % NA) * A_BYTES + a_block(wave, i) * 1024,
-          kbase + dchunk < K ? a_off[i] + (uint32_t)kbase : 0x80000000u);
+          kt < KT && kbyte + dchunk < K ? a_off[i] + (uint32_t)kbyte : 0x80000000u);
   };
   auto dma_b = [&](int kt, int j) {
     if constexpr (KALIGNED) {
       dma16s(rb, b_ring + (kt % NB) * B_BYTES + b_block(wave, j) * 1024, b_off[j],
-             (uint32_t)((kt < KT ? kt : KT - 1) * BK));
+             (uint32_t)((kbase + (kt < KT ? kt : KT - 1)) * BK));
       return;
     }
-    const int64_t kbase = (int64_t)kt * BK;
+    const int64_t kbyte = (int64_t)(kbase + kt) * BK;
     dma16(rb, b_ring + (kt % NB) * B_BYTES + b_block(wave, j) * 1024,
-          kbase + dchunk < K ? b_off[j] + (uint32_t)kbase : 0x80000000u);
+          kt < KT && kbyte + dchunk < K ? b_off[j] + (uint32_t)kbyte : 0x80000000u);
   };
   auto issue_a = [&](int kt) {
 #pragma unroll
@@ -618,13 +631,13 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_fast(GemmArgs p) 
     // DMAs past the last k-step re-read the last one (every address stays in
     // the panel) into slots that no k-step reads again.
     auto pdma_a = [&](int kt) {
-      const uint32_t soff = (uint32_t)((kt < KT ? kt : KT - 1) * BK);
+      const uint32_t soff = (uint32_t)((kbase + (kt < KT ? kt : KT - 1)) * BK);
 #pragma unroll
       for (int i = 0; i < PA; ++i)
         dma16s(ra, a_ring + (kt % NA) * A_BYTES + (q * PA + i) * 1024, pa_off[i], soff);
     };
     auto pdma_b = [&](int kt) {
-      const uint32_t soff = (uint32_t)((kt < KT ? kt : KT - 1) * BK);
+      const uint32_t soff = (uint32_t)((kbase + (kt < KT ? kt : KT - 1)) * BK);
 #pragma unroll
       for (int j = 0; j < PB; ++j)
         dma16s(rb, b_ring + (kt % NB) * B_BYTES + (q * PB + j) * 1024, pb_off[j], soff);
@@ -877,6 +890,60 @@ __global__ __launch_bounds__(256) void gemm_generic(GemmArgs p) {
     }
 }
 
+// ---------------------------------------------------- split-K reduce ----
+// out[m, n] = epilogue(sum_s part[s, m, n]): the slices of a split-K GEMM
+// added in int32 (exact), then the same dequant and epilogue arithmetic as
+// the one-pass kernels. With p.staged each thread finishes 8 consecutive
+// outputs of one row (32-byte partial loads per slice, one 16-byte store);
+// otherwise one output per thread.
+template <int EPI, bool BIAS>
+__global__ __launch_bounds__(256) void splitk_reduce(GemmArgs p, const int32_t* __restrict__ part,
+                                                     int splits) {
+  const int64_t mn = p.m * p.n;
+  const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (!p.staged) {
+    if (t >= mn) return;
+    int acc = 0;
+    for (int sl = 0; sl < splits; ++sl) acc += part[sl * mn + t];
+    store_scalar<EPI, BIAS>(p, t / p.n, t % p.n, acc);
+    return;
+  }
+  const int64_t per_row = p.n / 8;
+  if (t >= p.m * per_row) return;
+  const int64_t row = t / per_row, col = (t - row * per_row) * 8;
+  const int64_t o = row * p.n + col;
+  int acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  for (int sl = 0; sl < splits; ++sl) {
+    const uint4* src = reinterpret_cast<const uint4*>(part + sl * mn + o);
+    const uint4 lo = load_nt(src), hi = load_nt(src + 1);
+    acc[0] += (int)lo.x; acc[1] += (int)lo.y; acc[2] += (int)lo.z; acc[3] += (int)lo.w;
+    acc[4] += (int)hi.x; acc[5] += (int)hi.y; acc[6] += (int)hi.z; acc[7] += (int)hi.w;
+  }
+  if (EPI == EPI_RAW) {
+    uint4* dst = reinterpret_cast<uint4*>(static_cast<int32_t*>(p.c) + o);
+    store_nt(dst, make_uint4(acc[0], acc[1], acc[2], acc[3]));
+    store_nt(dst + 1, make_uint4(acc[4], acc[5], acc[6], acc[7]));
+    return;
+  }
+  const float rs = p.rs[row];
+  const float4 c0 = *reinterpret_cast<const float4*>(p.cs + col);
+  const float4 c1 = *reinterpret_cast<const float4*>(p.cs + col + 4);
+  const float cs[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+  float bias[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  if (BIAS) unpack8(*reinterpret_cast<const uint4*>(p.bias + col), bias);
+  float gate[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f}, x[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  if (EPI == EPI_GATED) {
+    const int64_t tr = table_row(p, row);
+    unpack8(*reinterpret_cast<const uint4*>(p.table + tr * p.table_width + (int64_t)p.gate_slot * p.n + col),
+            gate);
+    unpack8(load_nt(reinterpret_cast<const uint4*>(p.resid + o)), x);
+  }
+  float v[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) v[e] = finish<EPI>(dequant<BIAS>(acc[e], rs, cs[e], bias[e]), gate[e], x[e]);
+  store_c16(static_cast<uint16_t*>(p.c) + o, pack8(v));
+}
+
 // ------------------------------------------------------------- launch ----
 struct FastCfg {
   int bm, bn;
@@ -887,7 +954,7 @@ template <int BM, int BN, int WAVES_M, int WAVES_N, int EPI, bool BIAS, int NA =
 void launch_fast_cfg(GemmArgs& p, hipStream_t st) {
   p.tiles_m = (int)((p.m + BM - 1) / BM);
   p.tiles_n = (int)((p.n + BN - 1) / BN);
-  const unsigned grid = (unsigned)(p.tiles_m * p.tiles_n);
+  const unsigned grid = (unsigned)(p.tiles_m * p.tiles_n * p.splits);
   constexpr bool kPingPong = GEMM_PINGPONG && WAVES_M * WAVES_N == 8 && NA == 3 && NB == 2;
   if (p.k % 128 == 0)
     hipLaunchKernelGGL((gemm_fast<BM, BN, WAVES_M, WAVES_N, EPI, BIAS, NA, NB, true, kPingPong>),
@@ -969,6 +1036,25 @@ void launch_generic(GemmArgs& p, hipStream_t st) {
   hipLaunchKernelGGL((gemm_generic<EPI, BIAS>), grid, dim3(256), 0, st, p);
 }
 
+// The split-K pass: the tile's raw-int32 kernel over tiles x splits workgroups
+// into the workspace, then splitk_reduce with the caller's epilogue.
+template <int EPI, bool BIAS>
+void launch_split(int tile, GemmArgs p, int32_t* ws, hipStream_t st) {
+  GemmArgs q = p;
+  q.c = ws;
+  q.bias = nullptr;
+  q.nvec = 1;  // N % 4 == 0 and a 256-byte aligned workspace
+  q.staged = 0;
+  launch_fast<EPI_RAW, false>(tile, q, st);
+  const int splits = p.splits;
+  p.splits = 1;
+  // The 8-wide vector path also loads bias as 16-byte rows.
+  p.staged = p.staged && (!BIAS || aligned(p.bias, 16));
+  const int64_t threads = p.staged ? p.m * (p.n / 8) : p.m * p.n;
+  hipLaunchKernelGGL((splitk_reduce<EPI, BIAS>), dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, st,
+                     p, (const int32_t*)ws, splits);
+}
+
 template <int EPI>
 void dispatch_bias(bool generic, int tile, bool bias, GemmArgs& p, hipStream_t st) {
   if (generic) {
@@ -1040,22 +1126,68 @@ int auto_tile(int64_t m, int64_t n, int64_t k) {
   return c128 <= c64 ? LR_TILE_128x128 : LR_TILE_64x128;
 }
 
+// Split-K for a few hundred rows at long K, on 128x160 tiles: as many slices
+// as keep the workgroups within one wave of 256 CUs, at most 4 (1 = no split).
+// Graph-replayed at M = 256, N = 5120, K = 20480 (bf16 + bias): 35.6 us for
+// 128x160 in 4 slices against 41.8 us unsplit on the shape's own tile. At
+// K = 5120 every split measured slower than the unsplit small-M tiles (the
+// partial slices' write and re-read, and the second launch, cost more than
+// the shorter k-loops save).
+int auto_splits(int64_t m, int64_t n, int64_t k) {
+  if (m > 256 || k < 16384 || k % 128 != 0 || n % 4 != 0) return 1;
+  const int64_t tiles = ((m + 127) / 128) * ((n + 159) / 160);
+  int64_t s = 256 / tiles;
+  if (s > 4) s = 4;
+  return s > 1 ? (int)s : 1;
+}
+
 }  // namespace
 }  // namespace lr
 
 using namespace lr;
 
-extern "C" int lr_int8_gemm(const int8_t* a, const int8_t* b, int64_t b_stride_k,
-                            int64_t b_stride_n, int64_t m, int64_t n, int64_t k,
-                            const float* row_scale, const float* col_scale, const void* bias,
-                            void* c, int epilogue, const void* residual, const void* table,
-                            int64_t table_rows, int64_t table_width, const int64_t* indices,
-                            int64_t sequence, int gate_slot, int tile, void* stream) {
+namespace lr {
+namespace {
+
+// True when the MFMA fast path can run (W stored [N,K] row-major with 16-byte
+// aligned rows; buffer descriptors need per-block ranges below 2^31 bytes).
+bool fast_path(const int8_t* a, const int8_t* b, int64_t b_stride_k, int64_t b_stride_n, int64_t k,
+               int tile) {
+  return b_stride_k == 1 && b_stride_n == k && k % 16 == 0 && k > 0 && aligned(a, 16) &&
+         aligned(b, 16) && k <= (1LL << 22) && tile != LR_TILE_GENERIC;
+}
+
+struct Plan {
+  int tile;
+  int splits;
+};
+
+// The fast-path schedule: the tile (LR_TILE_AUTO: by shape) and the split-K
+// factor (splits 0: by shape when a workspace is allowed, else 1).
+Plan plan(int64_t m, int64_t n, int64_t k, int tile, int splits, bool workspace) {
+  Plan pl{tile == LR_TILE_AUTO ? auto_tile(m, n, k) : tile, splits > 0 ? splits : 1};
+  if (splits == 0 && workspace && tile == LR_TILE_AUTO) {
+    const int s = auto_splits(m, n, k);
+    if (s > 1) pl = Plan{LR_TILE_128x160, s};
+  }
+  return pl;
+}
+
+int64_t split_workspace(int64_t m, int64_t n, int splits) { return splits > 1 ? splits * m * n * 4 : 0; }
+
+int gemm_impl(const int8_t* a, const int8_t* b, int64_t b_stride_k, int64_t b_stride_n, int64_t m,
+              int64_t n, int64_t k, const float* row_scale, const float* col_scale, const void* bias,
+              void* c, int epilogue, const void* residual, const void* table, int64_t table_rows,
+              int64_t table_width, const int64_t* indices, int64_t sequence, int gate_slot,
+              void* workspace, int64_t workspace_bytes, int splits, int tile, void* stream) {
   LR_REQUIRE(m >= 0 && n >= 0 && k >= 0, "int8_gemm: negative shape");
   LR_REQUIRE(epilogue >= LR_EPI_BF16 && epilogue <= LR_EPI_RAW_INT32,
              "int8_gemm: unknown epilogue %d", epilogue);
   LR_REQUIRE(tile >= LR_TILE_AUTO && tile <= LR_TILE_256x256_PERSISTENT, "int8_gemm: unknown tile %d",
              tile);
+  LR_REQUIRE(splits >= 0 && splits <= 64, "int8_gemm: splits %d outside 0..64", splits);
+  LR_REQUIRE(workspace_bytes >= 0 && (workspace != nullptr || workspace_bytes == 0),
+             "int8_gemm: bad workspace");
   if (m == 0 || n == 0) return LR_OK;
   LR_REQUIRE(a && b && c, "int8_gemm: null A/B/C");
   if (epilogue != LR_EPI_RAW_INT32) LR_REQUIRE(row_scale && col_scale, "int8_gemm: null scales");
@@ -1074,6 +1206,7 @@ extern "C" int lr_int8_gemm(const int8_t* a, const int8_t* b, int64_t b_stride_k
   p.table_rows = table_rows; p.table_width = table_width; p.sequence = sequence;
   p.gate_slot = gate_slot;
   p.group_m = GEMM_GROUP_M;
+  p.splits = 1;
   p.nvec = n % 4 == 0 && aligned(c, epilogue == LR_EPI_RAW_INT32 ? 16 : 8) &&
            (epilogue == LR_EPI_RAW_INT32 || aligned(col_scale, 16)) &&
            (bias == nullptr || aligned(bias, 8)) &&
@@ -1084,21 +1217,50 @@ extern "C" int lr_int8_gemm(const int8_t* a, const int8_t* b, int64_t b_stride_k
              (epilogue != LR_EPI_GATED_RESIDUAL ||
               (aligned(residual, 16) && aligned(table, 16) && table_width % 8 == 0));
 
-  // Fast path: W stored [N,K] row-major with 16-byte aligned rows; buffer
-  // descriptors need per-block ranges (256 rows * K) below 2^31 bytes.
-  const bool fast = b_stride_k == 1 && b_stride_n == k && k % 16 == 0 && k > 0 &&
-                    aligned(a, 16) && aligned(b, 16) && k <= (1LL << 22) &&
-                    tile != LR_TILE_GENERIC;
+  const bool fast = fast_path(a, b, b_stride_k, b_stride_n, k, tile);
+  int32_t* ws = nullptr;
   if (!fast) {
     LR_REQUIRE((m + 63) / 64 <= 65535, "int8_gemm: generic path supports M <= 4194240");
+    LR_REQUIRE(splits <= 1, "int8_gemm: split-K needs the MFMA fast path");
   } else {
-    if (tile == LR_TILE_AUTO) tile = auto_tile(m, n, k);
+    const Plan pl = plan(m, n, k, tile, splits, workspace != nullptr);
+    tile = pl.tile;
     const int64_t tiles = ((m + tile_rows(tile) - 1) / tile_rows(tile)) *
                           ((n + tile_cols(tile) - 1) / tile_cols(tile));
-    LR_REQUIRE(tiles <= 0x7fffffffLL, "int8_gemm: too many tiles");
+    LR_REQUIRE(tiles * pl.splits <= 0x7fffffffLL, "int8_gemm: too many tiles");
+    if (pl.splits > 1) {
+      LR_REQUIRE(tile != LR_TILE_256x256_PERSISTENT, "int8_gemm: the persistent tile does not split K");
+      LR_REQUIRE(k % 128 == 0 && pl.splits <= k / 128,
+                 "int8_gemm: split-K needs K %% 128 == 0 and at most K / 128 splits");
+      LR_REQUIRE(n % 4 == 0, "int8_gemm: split-K needs N %% 4 == 0");
+      const int64_t need = split_workspace(m, n, pl.splits);
+      LR_REQUIRE(workspace_bytes >= need, "int8_gemm: %d-way split-K needs a %lld-byte workspace, got %lld",
+                 pl.splits, (long long)need, (long long)workspace_bytes);
+      LR_REQUIRE(aligned(workspace, 256), "int8_gemm: workspace must be 256-byte aligned");
+      ws = static_cast<int32_t*>(workspace);
+      p.splits = pl.splits;
+    }
   }
   hipStream_t st = as_stream(stream);
   const bool has_bias = bias != nullptr && epilogue != LR_EPI_RAW_INT32;
+  if (ws != nullptr) {
+    switch (epilogue) {
+      case LR_EPI_BF16:
+        if (has_bias) launch_split<EPI_BF16, true>(tile, p, ws, st);
+        else launch_split<EPI_BF16, false>(tile, p, ws, st);
+        break;
+      case LR_EPI_GELU_TANH:
+        if (has_bias) launch_split<EPI_GELU, true>(tile, p, ws, st);
+        else launch_split<EPI_GELU, false>(tile, p, ws, st);
+        break;
+      case LR_EPI_GATED_RESIDUAL:
+        if (has_bias) launch_split<EPI_GATED, true>(tile, p, ws, st);
+        else launch_split<EPI_GATED, false>(tile, p, ws, st);
+        break;
+      default: launch_split<EPI_RAW, false>(tile, p, ws, st); break;
+    }
+    return check_launch("int8_gemm");
+  }
   switch (epilogue) {
     case LR_EPI_BF16: dispatch_bias<EPI_BF16>(!fast, tile, has_bias, p, st); break;
     case LR_EPI_GELU_TANH: dispatch_bias<EPI_GELU>(!fast, tile, has_bias, p, st); break;
@@ -1106,4 +1268,37 @@ extern "C" int lr_int8_gemm(const int8_t* a, const int8_t* b, int64_t b_stride_k
     default: dispatch_bias<EPI_RAW>(!fast, tile, false, p, st); break;
   }
   return check_launch("int8_gemm");
+}
+
+}  // namespace
+}  // namespace lr
+
+extern "C" int lr_int8_gemm(const int8_t* a, const int8_t* b, int64_t b_stride_k,
+                            int64_t b_stride_n, int64_t m, int64_t n, int64_t k,
+                            const float* row_scale, const float* col_scale, const void* bias,
+                            void* c, int epilogue, const void* residual, const void* table,
+                            int64_t table_rows, int64_t table_width, const int64_t* indices,
+                            int64_t sequence, int gate_slot, int tile, void* stream) {
+  return gemm_impl(a, b, b_stride_k, b_stride_n, m, n, k, row_scale, col_scale, bias, c, epilogue,
+                   residual, table, table_rows, table_width, indices, sequence, gate_slot, nullptr, 0,
+                   1, tile, stream);
+}
+
+extern "C" int lr_int8_gemm_ws(const int8_t* a, const int8_t* b, int64_t b_stride_k,
+                               int64_t b_stride_n, int64_t m, int64_t n, int64_t k,
+                               const float* row_scale, const float* col_scale, const void* bias,
+                               void* c, int epilogue, const void* residual, const void* table,
+                               int64_t table_rows, int64_t table_width, const int64_t* indices,
+                               int64_t sequence, int gate_slot, void* workspace,
+                               int64_t workspace_bytes, int splits, int tile, void* stream) {
+  return gemm_impl(a, b, b_stride_k, b_stride_n, m, n, k, row_scale, col_scale, bias, c, epilogue,
+                   residual, table, table_rows, table_width, indices, sequence, gate_slot, workspace,
+                   workspace_bytes, splits, tile, stream);
+}
+
+extern "C" int64_t lr_int8_gemm_workspace_size(int64_t m, int64_t n, int64_t k, int splits, int tile) {
+  if (m <= 0 || n <= 0 || k <= 0 || k % 128 != 0 || n % 4 != 0 || splits < 0 || splits > 64 ||
+      tile < LR_TILE_AUTO || tile > LR_TILE_256x256_PERSISTENT || tile == LR_TILE_GENERIC)
+    return 0;
+  return split_workspace(m, n, plan(m, n, k, tile, splits, true).splits);
 }

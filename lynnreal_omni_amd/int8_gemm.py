@@ -65,22 +65,38 @@ def _torch_matmul(a, b, row_scale, column_scale, bias):
 
 
 def _launch(a, b, row_scale, column_scale, bias, out, epilogue, tile, residual=None, table=None,
-            indices=None, sequence=0, gate_slot=0):
+            indices=None, sequence=0, gate_slot=0, splits=None):
     m, k = a.shape
     n = b.shape[1]
     table_rows = table_width = 0
     if table is not None:
         table_width = table.shape[-1]
         table_rows = table.numel() // table_width
-    _lib.call("lr_int8_gemm", a.data_ptr(), b.data_ptr(), b.stride(0), b.stride(1), m, n, k,
+    tile_id = _tile_id(tile)
+    splits = 0 if splits is None else int(splits)
+    ws, ws_bytes = _lib.workspace(a, _workspace_bytes(m, n, k, splits, tile_id))
+    _lib.call("lr_int8_gemm_ws", a.data_ptr(), b.data_ptr(), b.stride(0), b.stride(1), m, n, k,
               _lib.ptr(row_scale), _lib.ptr(column_scale), _lib.ptr(bias), out.data_ptr(),
               epilogue, _lib.ptr(residual), _lib.ptr(table), table_rows, table_width,
-              _lib.ptr(indices), sequence, gate_slot, _tile_id(tile), _lib.stream(a))
+              _lib.ptr(indices), sequence, gate_slot, ws, ws_bytes, splits, tile_id, _lib.stream(a))
     return out
 
 
+_ws_sizes: dict[tuple, int] = {}
+
+
+def _workspace_bytes(m, n, k, splits, tile_id) -> int:
+    """Workspace bytes of the library's split-K schedule for this shape (0
+    when it does not split K), cached per shape."""
+    key = (m, n, k, splits, tile_id)
+    size = _ws_sizes.get(key)
+    if size is None:
+        size = _ws_sizes[key] = int(_lib.load().lr_int8_gemm_workspace_size(m, n, k, splits, tile_id))
+    return size
+
+
 def int8_matmul(a, b, row_scale, column_scale, bias=None, *, tile=None, activation=None,
-                residual=None, table=None, indices=None, gate_slot=None):
+                residual=None, table=None, indices=None, gate_slot=None, splits=None):
     """bf16(((float)(a @ b) * row_scale) * column_scale + bias) on MFMA.
 
     a int8 [M, K] contiguous; b int8 [K, N] with any strides (the weight
@@ -123,21 +139,21 @@ def int8_matmul(a, b, row_scale, column_scale, bias=None, *, tile=None, activati
         if indices.numel() < sequence:
             raise ValueError("indices shorter than the sequence")
         return _launch(a, b, row_scale, column_scale, bias, output, _lib.EPI_GATED_RESIDUAL, tile,
-                       residual, table, indices, sequence, int(gate_slot))
+                       residual, table, indices, sequence, int(gate_slot), splits=splits)
     if activation is None:
         epilogue = _lib.EPI_BF16
     elif activation == "gelu_tanh":
         epilogue = _lib.EPI_GELU_TANH
     else:
         raise ValueError(f"unsupported activation {activation!r}")
-    return _launch(a, b, row_scale, column_scale, bias, output, epilogue, tile)
+    return _launch(a, b, row_scale, column_scale, bias, output, epilogue, tile, splits=splits)
 
 
-def int8_matmul_int32(a, b, *, tile=None):
+def int8_matmul_int32(a, b, *, tile=None, splits=None):
     """Raw int32 accumulators a @ b of the same MFMA kernel (parity/debug)."""
     if a.dtype != torch.int8 or b.dtype != torch.int8 or not a.is_contiguous() or a.shape[1] != b.shape[0]:
         raise ValueError("INT8 GEMM requires contiguous row-major activations and compatible INT8 weights")
     _lib.check_device(a)
     _lib.same_device(a, b=b)
     out = torch.empty((a.shape[0], b.shape[1]), device=a.device, dtype=torch.int32)
-    return _launch(a, b, None, None, None, out, _lib.EPI_RAW_INT32, tile)
+    return _launch(a, b, None, None, None, out, _lib.EPI_RAW_INT32, tile, splits=splits)

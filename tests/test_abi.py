@@ -18,7 +18,7 @@ HEADER = ROOT / "include" / "lynnreal_amd.h"
 
 def declared():
     text = HEADER.read_text()
-    return sorted(set(re.findall(r"^(?:int|const char\*)\s+(lr_\w+)\(", text, re.M)))
+    return sorted(set(re.findall(r"^(?:int|int64_t|const char\*)\s+(lr_\w+)\(", text, re.M)))
 
 
 @pytest.fixture(scope="module")
@@ -56,7 +56,7 @@ def test_exported_symbols_are_exactly_the_declared_ones(lib):
 
 
 def test_python_prototypes_are_exactly_the_declared_ones():
-    names = set(declared()) - {"lr_last_error"}
+    names = set(declared()) - {"lr_last_error", "lr_int8_gemm_workspace_size"}
     assert set(_lib.SIGNATURES) == names
 
 
@@ -103,3 +103,23 @@ def test_missing_library_fails_loudly(monkeypatch, tmp_path):
     monkeypatch.setenv("LYNNREAL_AMD_LIBRARY", str(tmp_path / "absent.so"))
     with pytest.raises(RuntimeError, match="no CPU fallback"):
         _lib.load()
+
+
+def test_split_k_workspace_sizes_and_checks_without_a_gpu(lib):
+    """lr_int8_gemm_workspace_size: S x M x N int32 slices for a split-K
+    schedule, 0 otherwise; lr_int8_gemm_ws refuses a forced split without
+    room for its slices before any launch."""
+    size = lib.lr_int8_gemm_workspace_size
+    assert size(256, 5120, 5120, 1, _lib.TILE_AUTO) == 0
+    assert size(256, 5120, 5120, 4, _lib.TILE_AUTO) == 4 * 256 * 5120 * 4
+    assert size(256, 5120, 20480, 0, _lib.TILE_AUTO) == 4 * 256 * 5120 * 4  # auto: long K, M <= 256
+    assert size(256, 5120, 5120, 0, _lib.TILE_AUTO) == 0
+    assert size(12288, 5120, 20480, 0, _lib.TILE_AUTO) == 0
+    assert size(256, 5120, 5136, 2, _lib.TILE_AUTO) == 0                     # K % 128 != 0
+    p = ctypes.c_void_p(256)  # never dereferenced: validation fails first
+    rc = lib.lr_int8_gemm_ws(p, p, 1, 1024, 64, 128, 1024, p, p, None, p, 0, None, None, 0, 0, None, 0, 0,
+                             None, 0, 2, _lib.TILE_AUTO, None)
+    assert rc == _lib.LR_EINVAL and b"workspace" in lib.lr_last_error()
+    rc = lib.lr_int8_gemm_ws(p, p, 1, 1024, 64, 128, 1024, p, p, None, p, 0, None, None, 0, 0, None, 0, 0,
+                             None, 0, 65, _lib.TILE_AUTO, None)
+    assert rc == _lib.LR_EINVAL and b"splits" in lib.lr_last_error()
