@@ -130,6 +130,22 @@ int lr_int8_gemm_ws(const int8_t* a, const int8_t* b, int64_t b_stride_k, int64_
  * the reference has no counterpart (its Triton GEMM keeps no partials). */
 int64_t lr_int8_gemm_workspace_size(int64_t m, int64_t n, int64_t k, int splits, int tile);
 
+/* lr_int8_gemm_ws without the workspace: the split-K slices go to a
+ * file-scope device array of the library (32 MiB, one per GPU, held until
+ * the process ends), so the call allocates nothing and takes no workspace.
+ * No counterpart in the reference: it is for callers that cannot allocate
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). A split whose slices need more than 32 MiB is refused with
+ * LR_EINVAL (the automatic choice needs at most about 21 MiB); calls that
+ * overlap on one GPU share the array and race. Same arguments, arithmetic
+ * and outputs as lr_int8_gemm_ws. */
+int lr_int8_gemm_noalloc(const int8_t* a, const int8_t* b, int64_t b_stride_k, int64_t b_stride_n,
+                         int64_t m, int64_t n, int64_t k, const float* row_scale,
+                         const float* col_scale, const void* bias, void* c, int epilogue,
+                         const void* residual, const void* table, int64_t table_rows,
+                         int64_t table_width, const int64_t* indices, int64_t sequence,
+                         int gate_slot, int splits, int tile, void* stream);
+
 /* Stand-alone INT32 -> bf16 dequant epilogue.
  * Replaces model/kernels.py:41-46 (int8_epilogue):
  *   out[m,n] = bf16(((float)acc[m,n] * a_scale[m]) * w_scale[n] + bias[n]).

@@ -41,6 +41,8 @@ SIGNATURES = {
                      _I64, _P, _I64, _I32, _I32, _P],
     "lr_int8_gemm_ws": [_P, _P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _I32, _P, _P, _I64,
                         _I64, _P, _I64, _I32, _P, _I64, _I32, _I32, _P],
+    "lr_int8_gemm_noalloc": [_P, _P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _I32, _P, _P, _I64,
+                             _I64, _P, _I64, _I32, _I32, _I32, _P],
     "lr_int8_epilogue": [_P, _P, _P, _P, _P, _I64, _I64, _P],
     "lr_rms_adaln": [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I32, _I32, _F32, _P],
     "lr_rms_adaln_quant": [_P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I32, _I32,

@@ -23,6 +23,8 @@
 //    tiles and its 4 MB L2 holds the A and W panels its CUs share.
 // Generic kernel: any W strides / K, LDS-tiled int32 dot products (slow path
 // used only when the fast kernel cannot run).
+#include <mutex>
+
 #include "lr_device.h"
 #include "lr_runtime.h"
 
@@ -1294,6 +1296,70 @@ extern "C" int lr_int8_gemm_ws(const int8_t* a, const int8_t* b, int64_t b_strid
   return gemm_impl(a, b, b_stride_k, b_stride_n, m, n, k, row_scale, col_scale, bias, c, epilogue,
                    residual, table, table_rows, table_width, indices, sequence, gate_slot, workspace,
                    workspace_bytes, splits, tile, stream);
+}
+
+// ------------------------------------------------ allocation-free entry ----
+// Scratch of lr_int8_gemm_noalloc: the split-K slices for callers that cannot
+// allocate (code under graph capture, tight serving loops). Each GPU the
+// library runs on holds its own copy until the process ends. Every call on a
+// GPU shares that GPU's copy, so calls that overlap on one GPU race. Nothing
+// in it has to start at zero: each slice element is written by its split
+// before the reduce kernel reads it.
+constexpr int64_t kScratchBytes = 32LL << 20;
+static __device__ __align__(256) char scratch[kScratchBytes];
+
+namespace {
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[64];
+
+// The device address of `scratch` on the stream's device, looked up once per
+// device with that device current (in host code the array's name is a
+// host-side stand-in, not a device address).
+int scratch_address(hipStream_t st, void** out) {
+  int dev = 0;
+  hipError_t e = hipStreamGetDevice(st, &dev);
+  if (e != hipSuccess) return hip_fail(e, "int8_gemm_noalloc: hipStreamGetDevice");
+  if (dev < 0 || dev >= 64) return fail(LR_EUNSUPPORTED, "int8_gemm_noalloc: device %d not supported", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    int current = 0;
+    e = hipGetDevice(&current);
+    if (e != hipSuccess) return hip_fail(e, "int8_gemm_noalloc: hipGetDevice");
+    if (current != dev && (e = hipSetDevice(dev)) != hipSuccess)
+      return hip_fail(e, "int8_gemm_noalloc: hipSetDevice");
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    const hipError_t back = current != dev ? hipSetDevice(current) : hipSuccess;
+    if (e != hipSuccess) return hip_fail(e, "int8_gemm_noalloc: hipGetSymbolAddress(scratch)");
+    if (back != hipSuccess) return hip_fail(back, "int8_gemm_noalloc: hipSetDevice");
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return LR_OK;
+}
+}  // namespace
+
+extern "C" int lr_int8_gemm_noalloc(const int8_t* a, const int8_t* b, int64_t b_stride_k,
+                                    int64_t b_stride_n, int64_t m, int64_t n, int64_t k,
+                                    const float* row_scale, const float* col_scale, const void* bias,
+                                    void* c, int epilogue, const void* residual, const void* table,
+                                    int64_t table_rows, int64_t table_width, const int64_t* indices,
+                                    int64_t sequence, int gate_slot, int splits, int tile,
+                                    void* stream) {
+  LR_REQUIRE(splits >= 0 && splits <= 64, "int8_gemm: splits %d outside 0..64", splits);
+  const int64_t need = m > 0 && n > 0 && k > 0 ? lr_int8_gemm_workspace_size(m, n, k, splits, tile) : 0;
+  LR_REQUIRE(need <= kScratchBytes,
+             "int8_gemm_noalloc: this split needs %lld bytes of scratch, above the %lld-byte maximum "
+             "(lr_int8_gemm_ws takes a workspace of any size)",
+             (long long)need, (long long)kScratchBytes);
+  void* ws = nullptr;
+  if (need > 0) {
+    const int rc = scratch_address(as_stream(stream), &ws);
+    if (rc != LR_OK) return rc;
+  }
+  return gemm_impl(a, b, b_stride_k, b_stride_n, m, n, k, row_scale, col_scale, bias, c, epilogue,
+                   residual, table, table_rows, table_width, indices, sequence, gate_slot, ws,
+                   need > 0 ? kScratchBytes : 0, splits, tile, stream);
 }
 
 extern "C" int64_t lr_int8_gemm_workspace_size(int64_t m, int64_t n, int64_t k, int splits, int tile) {
