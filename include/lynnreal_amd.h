@@ -84,6 +84,18 @@ int lr_device_supported(int device);
 int lr_quantize_rows(const void* x, int64_t rows, int64_t width, int8_t* q, float* scales,
                      void* stream);
 
+/* Element types of lr_quantize_rows_typed. */
+#define LR_DTYPE_BF16 0
+#define LR_DTYPE_F16 1
+#define LR_DTYPE_F32 2
+
+/* lr_quantize_rows for bf16, fp16 or fp32 rows x (LR_DTYPE_*): the
+ * reference's Triton quantizer loads any float row as fp32
+ * (model/kernels.py:8-16); the scale and the IEEE quotient x / s are the
+ * same as for bf16 rows. */
+int lr_quantize_rows_typed(const void* x, int dtype, int64_t rows, int64_t width, int8_t* q,
+                           float* scales, void* stream);
+
 /* INT8 x INT8 -> INT32 GEMM with a fused epilogue.
  * Replaces model/int8_gemm.py:96-163 (int8_matmul) and its Triton kernel
  * model/int8_gemm.py:13-46:

@@ -24,6 +24,7 @@ LIBRARY = pathlib.Path(__file__).resolve().parent / "liblynnreal_amd.so"
 
 LR_OK, LR_EINVAL, LR_EUNSUPPORTED, LR_EHIP, LR_ENOMEM = 0, 1, 2, 3, 4
 EPI_BF16, EPI_GELU_TANH, EPI_GATED_RESIDUAL, EPI_RAW_INT32 = 0, 1, 2, 3
+DTYPE_BF16, DTYPE_F16, DTYPE_F32 = 0, 1, 2
 (TILE_AUTO, TILE_256x256, TILE_256x128, TILE_128x256, TILE_128x128, TILE_64x128, TILE_GENERIC,
  TILE_256x256_W4x2, TILE_256x192, TILE_256x80, TILE_64x80, TILE_128x160, TILE_192x256,
  TILE_256x256_PERSISTENT) = range(14)
@@ -37,6 +38,7 @@ _F32 = ctypes.c_float
 # name -> argument types (every entry point returns int).
 SIGNATURES = {
     "lr_quantize_rows": [_P, _I64, _I64, _P, _P, _P],
+    "lr_quantize_rows_typed": [_P, _I32, _I64, _I64, _P, _P, _P],
     "lr_int8_gemm": [_P, _P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _I32, _P, _P, _I64,
                      _I64, _P, _I64, _I32, _I32, _P],
     "lr_int8_gemm_ws": [_P, _P, _I64, _I64, _I64, _I64, _I64, _P, _P, _P, _P, _I32, _P, _P, _I64,
@@ -112,9 +114,17 @@ def raise_for(status: int, name: str) -> None:
     raise RuntimeError(message)
 
 
+_entry: dict[str, object] = {}
+
+
 def call(name: str, *args) -> None:
     """Call entry point `name` and raise on a non-zero status."""
-    raise_for(getattr(load(), name)(*args), name)
+    fn = _entry.get(name)
+    if fn is None:
+        fn = _entry[name] = getattr(load(), name)
+    status = fn(*args)
+    if status:
+        raise_for(status, name)
 
 
 _checked_devices: dict[int, bool] = {}
@@ -122,9 +132,9 @@ _checked_devices: dict[int, bool] = {}
 
 def check_device(t: torch.Tensor) -> None:
     """Raise unless `t` lives on a gfx950 GPU the library supports."""
-    if t.device.type != "cuda":
+    if not t.is_cuda:
         raise ValueError(f"the W8A8 HIP path needs GPU tensors, got a tensor on {t.device}")
-    index = t.device.index if t.device.index is not None else torch.cuda.current_device()
+    index = t.get_device()
     ok = _checked_devices.get(index)
     if ok is None:
         ok = _checked_devices[index] = bool(load().lr_device_supported(index))
@@ -137,13 +147,19 @@ def same_device(primary: torch.Tensor, **tensors) -> None:
     """Raise ValueError unless every tensor given (None is skipped) lives on
     `primary`'s device. The kernels receive raw pointers, so a host tensor or
     one on another GPU must be refused here, before any launch."""
+    index = primary.get_device()
     for name, t in tensors.items():
-        if t is not None and t.device != primary.device:
+        if t is not None and t.get_device() != index:
             raise ValueError(f"{name} is on {t.device}, but the kernel runs on {primary.device}")
+
+
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
 
 
 def stream(t: torch.Tensor) -> int:
     """The caller's current HIP stream on t's device (Triton's launch behaviour)."""
+    if _raw_stream is not None:
+        return _raw_stream(t.get_device())
     return torch.cuda.current_stream(t.device).cuda_stream
 
 
@@ -163,7 +179,7 @@ def workspace(t: torch.Tensor, nbytes: int) -> tuple[int | None, int]:
     replaced buffer only behind the work already queued on that stream."""
     if nbytes <= 0:
         return None, 0
-    key = (t.device.index if t.device.index is not None else torch.cuda.current_device(), stream(t))
+    key = (t.get_device(), stream(t))
     buf = _workspaces.get(key)
     if buf is None or buf.numel() < nbytes:
         buf = torch.empty(nbytes, dtype=torch.uint8, device=t.device)

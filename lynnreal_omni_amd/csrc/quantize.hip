@@ -90,6 +90,32 @@ __global__ __launch_bounds__(kThreads) void quantize_rows_any(const uint16_t* __
   if (threadIdx.x == 0) scales[row] = s;
 }
 
+// fp16 and fp32 rows (the reference's Triton quantizer loads any float type
+// as fp32, model/kernels.py:12): the same scale, and the IEEE quotient x / s
+// itself (the corrected-reciprocal form above is proven for bf16 values
+// only). One block per row, two passes over the row (the second from L2).
+template <typename T>
+__device__ __forceinline__ float as_float(T v) { return (float)v; }
+
+template <typename T>
+__global__ __launch_bounds__(kThreads) void quantize_rows_typed(const T* __restrict__ x,
+                                                                int8_t* __restrict__ q,
+                                                                float* __restrict__ scales,
+                                                                int64_t width) {
+  __shared__ float red[4];
+  const int64_t row = blockIdx.x;
+  const T* src = x + row * width;
+  float m = 0.0f;
+  for (int64_t c = threadIdx.x; c < width; c += kThreads) m = fmaxf(m, __builtin_fabsf(as_float(src[c])));
+  m = block256_max(m, red);
+  const float s = quant_scale(m);
+  for (int64_t c = threadIdx.x; c < width; c += kThreads) {
+    const float v = __builtin_rintf(as_float(src[c]) / s);
+    q[row * width + c] = (int8_t)fminf(fmaxf(v, -127.0f), 127.0f);
+  }
+  if (threadIdx.x == 0) scales[row] = s;
+}
+
 template <int CPT>
 void launch_quant_vec(const void* x, int8_t* q, float* s, int64_t rows, int chunks,
                       hipStream_t st) {
@@ -188,6 +214,26 @@ extern "C" int lr_quantize_rows(const void* x, int64_t rows, int64_t width, int8
     hipLaunchKernelGGL(quantize_rows_any, dim3((unsigned)rows), dim3(kThreads), 0, st,
                        (const uint16_t*)x, q, scales, width);
   }
+  return check_launch("quantize_rows");
+}
+
+extern "C" int lr_quantize_rows_typed(const void* x, int dtype, int64_t rows, int64_t width,
+                                      int8_t* q, float* scales, void* stream) {
+  LR_REQUIRE(dtype == LR_DTYPE_BF16 || dtype == LR_DTYPE_F16 || dtype == LR_DTYPE_F32,
+             "quantize_rows: unknown dtype %d", dtype);
+  if (dtype == LR_DTYPE_BF16) return lr_quantize_rows(x, rows, width, q, scales, stream);
+  LR_REQUIRE(rows >= 0 && width >= 0, "quantize_rows: negative shape (%lld, %lld)",
+             (long long)rows, (long long)width);
+  if (rows == 0) return LR_OK;
+  LR_REQUIRE(x && q && scales, "quantize_rows: null pointer");
+  LR_REQUIRE(rows <= 0x7fffffffLL, "quantize_rows: too many rows (%lld)", (long long)rows);
+  hipStream_t st = as_stream(stream);
+  if (dtype == LR_DTYPE_F16)
+    hipLaunchKernelGGL(quantize_rows_typed<_Float16>, dim3((unsigned)rows), dim3(kThreads), 0, st,
+                       (const _Float16*)x, q, scales, width);
+  else
+    hipLaunchKernelGGL(quantize_rows_typed<float>, dim3((unsigned)rows), dim3(kThreads), 0, st,
+                       (const float*)x, q, scales, width);
   return check_launch("quantize_rows");
 }
 

@@ -95,6 +95,15 @@ def _workspace_bytes(m, n, k, splits, tile_id) -> int:
     return size
 
 
+def _f32_vector(t):
+    """t's values as contiguous fp32 in their storage order: t itself when it
+    already is (a contiguous [M], [M, 1] or [1, N] fp32 tensor), so that the
+    common call converts and copies nothing."""
+    if t.dtype == torch.float32 and t.is_contiguous():
+        return t
+    return t.reshape(-1).float().contiguous()
+
+
 def int8_matmul(a, b, row_scale, column_scale, bias=None, *, tile=None, activation=None,
                 residual=None, table=None, indices=None, gate_slot=None, splits=None):
     """bf16(((float)(a @ b) * row_scale) * column_scale + bias) on MFMA.
@@ -110,14 +119,15 @@ def int8_matmul(a, b, row_scale, column_scale, bias=None, *, tile=None, activati
                      residual=residual, table=table, indices=indices)
     m, k = a.shape
     n = b.shape[1]
-    row_scale = row_scale.reshape(-1).float().contiguous()
-    column_scale = column_scale.reshape(-1).float().contiguous()
+    row_scale = _f32_vector(row_scale)
+    column_scale = _f32_vector(column_scale)
     if row_scale.numel() != m or column_scale.numel() != n:
         raise ValueError("row_scale must have M entries and column_scale N entries")
     if bias is not None:
         if bias.dtype != torch.bfloat16:
             raise ValueError("bias must be bfloat16")
-        bias = bias.reshape(-1).contiguous()
+        if not bias.is_contiguous():
+            bias = bias.contiguous()
         if bias.numel() != n:
             raise ValueError("bias must have N entries")
     output = torch.empty((m, n), device=a.device, dtype=torch.bfloat16)

@@ -34,8 +34,12 @@ from . import _lib
 
 
 def _bf16(t: torch.Tensor, what: str) -> torch.Tensor:
+    """t contiguous, or RuntimeError("... not supported") for another dtype:
+    these kernels read bfloat16, and the error is one that
+    acceleration.optional_kernel_failure lets a caller fall back from (the
+    reference's Triton kernels load any float dtype, model/kernels.py:64,100,146)."""
     if t.dtype != torch.bfloat16:
-        raise ValueError(f"{what} must be bfloat16, got {t.dtype}")
+        raise RuntimeError(f"{what}: dtype {t.dtype} is not supported by the HIP kernel (bfloat16 only)")
     return t.contiguous()
 
 
@@ -62,15 +66,27 @@ def _norm_args(source, norm, table, indices):
     return source, weight, table, indices, hidden, sequence, width, table_rows
 
 
+_QUANT_DTYPES = {torch.bfloat16: _lib.DTYPE_BF16, torch.float16: _lib.DTYPE_F16,
+                 torch.float32: _lib.DTYPE_F32}
+
+
 def quantize_rows(value):
-    """Per-row symmetric INT8 quantizer (model/kernels.py:19-24)."""
+    """Per-row symmetric INT8 quantizer (model/kernels.py:19-24) for bf16,
+    fp16 or fp32 rows (the Triton kernel loads any float row as fp32)."""
     rows, width = value.shape
-    value = _bf16(value, "value")
+    dtype = _QUANT_DTYPES.get(value.dtype)
+    if dtype is None:
+        raise RuntimeError(f"value: dtype {value.dtype} is not supported by the HIP quantizer")
+    value = value.contiguous()
     _lib.check_device(value)
     output = torch.empty_like(value, dtype=torch.int8)
     scales = torch.empty(rows, 1, device=value.device, dtype=torch.float32)
-    _lib.call("lr_quantize_rows", value.data_ptr(), rows, width, output.data_ptr(),
-              scales.data_ptr(), _lib.stream(value))
+    if dtype == _lib.DTYPE_BF16:
+        _lib.call("lr_quantize_rows", value.data_ptr(), rows, width, output.data_ptr(),
+                  scales.data_ptr(), _lib.stream(value))
+    else:
+        _lib.call("lr_quantize_rows_typed", value.data_ptr(), dtype, rows, width, output.data_ptr(),
+                  scales.data_ptr(), _lib.stream(value))
     return output, scales
 
 

@@ -5,6 +5,7 @@ so the orchestration and the fused epilogues (residual + norm2 + quant, the
 FFN-down gated residual in the GEMM) change nothing; the time-modulation
 cache reuses tables per timestep key; a recoverable kernel failure falls
 back to the native block."""
+import numpy as np
 import pytest
 import torch
 
@@ -72,6 +73,74 @@ def test_fused_block_equals_unfused_sequence():
     assert report["residual_ffn_norm_fused"] and report["qk_ordered_reduction"]
     got = block(x, temb, idx, rotary)
     assert got.dtype == torch.bfloat16 and torch.equal(got, want)
+
+
+def _oracle_block(block, x, temb, idx, rotary):
+    """The same block composed from the oracle's functions (model/fusion.py:61-98,
+    fused_quant path), with the same attention stand-in fed the oracle's Q/K/V.
+    Returns (qkv, first residual, block output) as bf16 bit patterns."""
+    import torch.nn.functional as F
+    from helpers import from_np, to_np
+    from oracle import reference as ref
+
+    def layer(lin):
+        w_nk = lin.weight_int8.t().contiguous().cpu().numpy()
+        return w_nk, to_np(lin.weight_scale.float()).reshape(-1), to_np(lin.bias)
+
+    t = x.shape[-2]
+    eps = block.norm1.eps
+    lin = block.adaln_proj.linear
+    # the adaLN kernel's fused silu equals torch's own GPU F.silu (test_gpu_adaln.py)
+    table = ref.adaln_table(to_np(F.silu(temb).to(torch.bfloat16)), to_np(lin.weight), to_np(lin.bias))
+    xi, ii = to_np(x), idx.cpu().numpy()
+    q, s = ref.rms_adaln_quant(xi, to_np(block.norm1.weight), table, ii, 0, 1, eps)
+    qkv = ref.linear(q, s, *layer(block.attn.to_qkv)).reshape(1, t, 3 * DIM)
+    query, key, value = (qkv[..., i * DIM:(i + 1) * DIM].reshape(1, t, HEADS, DIM // HEADS) for i in range(3))
+    cos, sin = (c.float().cpu().numpy() for c in rotary)
+    qo, ko = ref.qk_norm_rope(query, key, to_np(block.attn.norm_q.weight), to_np(block.attn.norm_k.weight),
+                              cos, sin, block.attn.norm_q.eps)
+    dev = x.device
+    att = _attention(from_np(qo, dev), from_np(ko, dev), from_np(np.ascontiguousarray(value), dev), None, None)
+    qa, sa = ref.quantize_rows(to_np(att.flatten(2, 3)).reshape(t, DIM))
+    upd = ref.linear(qa, sa, *layer(block.attn.to_out[0])).reshape(1, t, DIM)
+    x1 = ref.gated_residual(xi, upd, table, ii, 2)
+    q2, s2 = ref.rms_adaln_quant(x1, to_np(block.norm2.weight), table, ii, 3, 4, eps)
+    proj = ref.linear(q2, s2, *layer(block.ff.net[0].proj))
+    q3, s3 = ref.swiglu_quant(proj)
+    y = ref.linear(q3, s3, *layer(block.ff.net[2])).reshape(1, t, DIM)
+    return qkv, x1, ref.gated_residual(x1, y, table, ii, 5)
+
+
+@torch.inference_mode()
+def test_fused_block_against_oracle_chain():
+    """fused_block against the block composed from the oracle's functions:
+    the QKV projection and the first gated residual bit for bit (the unfused
+    GPU sequence, which the fused block equals bit for bit, supplies those
+    intermediates), the block output within the SwiGLU tolerance (the
+    activation is within 2 bf16 ulp of the oracle's, so its int8 codes may
+    move by one)."""
+    from helpers import assert_bf16_close, to_np
+    block = _block(11)
+    x, temb, idx, rotary = _inputs(seed=12)
+    want_qkv, want_x1, want_out = _oracle_block(block, x, temb, idx, rotary)
+    lin = block.adaln_proj.linear
+    table = k.adaln_table(temb, lin.weight, lin.bias).view(-1, 6 * DIM)
+    q, s = k._rms_adaln_quant_int8(x, block.norm1, table, idx, 0, 1)
+    qkv = block.attn.to_qkv.forward_quantized(q, s, x.shape[:-1])
+    assert np.array_equal(to_np(qkv), want_qkv)
+    query, key, value = (t.unflatten(-1, (HEADS, -1)) for t in qkv.chunk(3, dim=-1))
+    qo, ko = k.qk_norm_rope(query, key, block.attn.norm_q.weight, block.attn.norm_k.weight, rotary,
+                            block.attn.norm_q.eps)
+    att = _attention(qo, ko, value, None, None).flatten(2, 3).type_as(qo)
+    qa, sa = k.quantize_rows(att.reshape(-1, DIM))
+    x1 = k._gated_residual(x, block.attn.to_out[0].forward_quantized(qa, sa, att.shape[:-1]), table, idx, 2)
+    assert np.array_equal(to_np(x1), want_x1)
+    unfused = _unfused(block, x, temb, idx, rotary)
+    fusion.enable_fusion(toy.Transformer([block]), fused_quant=True, attention=_attention)
+    got = block(x, temb, idx, rotary)
+    assert torch.equal(got, unfused)
+    # the north-star bar for bf16 outputs: max relative error <= 1e-2, cosine >= 0.9999
+    assert_bf16_close(to_np(got), want_out, max_ulp=64, frac_exact=0.5, rel=1e-2, cos=0.9999, atol=1e-3)
 
 
 @torch.inference_mode()

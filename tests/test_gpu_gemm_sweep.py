@@ -21,7 +21,7 @@ TILES = [None, (256, 256), "256x256_w4x2", (256, 192), (256, 80), (64, 80), (128
 EPILOGUES = ["int32", "bf16", "gelu_tanh", "gated"]
 
 
-def _cases(count=36, seed=20261202):
+def _cases(count=4 * len(TILES), seed=20261202):
     rng = np.random.default_rng(seed)
     out = []
     for i in range(count):
@@ -30,7 +30,9 @@ def _cases(count=36, seed=20261202):
         if i % 4 == 3:
             n += 4                                  # ... and N % 8 == 4 takes the direct stores
         k = int(rng.integers(1, 80)) * 16
-        # every tile meets every epilogue once over the 36 cases
+        # with T = len(TILES) = 14 tiles, tile t meets epilogues t, t + 3, t + 2 and
+        # t + 1 (mod 4) in cases t, t + T, t + 2T and t + 3T: every tile meets every
+        # epilogue once
         out.append((m, n, k, TILES[i % len(TILES)], EPILOGUES[(i + i // len(TILES)) % len(EPILOGUES)],
                     i % 3 != 0))
     return out

@@ -74,3 +74,42 @@ def test_int8_epilogue_bit_exact(m, n, bias):
 
 def test_golden_fixtures_on_gpu():
     golden_check.check_all(gpu.module)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
+@pytest.mark.parametrize("rows,width", [(64, 5120), (7, 1000), (3, 20480)])
+def test_quantize_rows_fp16_fp32_rows(dtype, rows, width):
+    """fp16 and fp32 rows (the Triton quantizer loads any float row as fp32,
+    model/kernels.py:12) against the torch restatement of model/int8.py:66-67
+    on the same values; the first row holds exact half-integer quotients."""
+    from lynnreal_omni_amd import kernels
+    from oracle import torch_path as tp
+    g = gen(rows * 31 + width)
+    x = torch.randn(rows, width, generator=g) * 3
+    x[:, ::97] *= 20
+    x[0] = torch.arange(width) % 255 - 127.0
+    x[0, 1::2] += 0.5
+    x[0, 0] = 127.0
+    x = x.to(dtype)
+    q, s = kernels.quantize_rows(x.cuda())
+    want_q, want_s = tp.quantize(x)
+    assert torch.equal(q.cpu(), want_q) and torch.equal(s.cpu(), want_s)
+
+
+def test_other_dtypes_are_recoverable_failures():
+    """The bf16-only row kernels refuse other float types with the error that
+    acceleration.optional_kernel_failure treats as recoverable, so the fused
+    block guard falls back instead of failing (model/fusion.py:101-116)."""
+    import types
+    from lynnreal_omni_amd import acceleration, kernels
+    x = torch.randn(1, 16, 64, device="cuda")
+    norm = types.SimpleNamespace(weight=torch.ones(64, device="cuda", dtype=torch.bfloat16), eps=1e-6)
+    table = torch.zeros(1, 6 * 64, device="cuda", dtype=torch.bfloat16)
+    idx = torch.zeros(16, dtype=torch.int64, device="cuda")
+    for call in (lambda: kernels._rms_adaln(x, norm, table, idx, 0, 1),
+                 lambda: kernels._rms_adaln_quant_int8(x, norm, table, idx, 0, 1),
+                 lambda: kernels._gated_residual(x, x.bfloat16(), table, idx, 2),
+                 lambda: kernels.quantize_rows(torch.zeros(4, 8, dtype=torch.float64, device="cuda"))):
+        with pytest.raises(RuntimeError, match="not supported") as err:
+            call()
+        assert acceleration.optional_kernel_failure(err.value)

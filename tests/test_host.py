@@ -78,14 +78,19 @@ def test_int8_matmul_validation():
 
 
 def test_kernel_wrappers_validate_before_launch():
-    with pytest.raises(ValueError, match="bfloat16"):
-        kernels.quantize_rows(torch.zeros(2, 8))
+    with pytest.raises(RuntimeError, match="not supported"):
+        kernels.quantize_rows(torch.zeros(2, 8, dtype=torch.float64))
+    with pytest.raises(ValueError, match="GPU tensors"):
+        kernels.quantize_rows(torch.zeros(2, 8))                    # fp32 rows are supported
     with pytest.raises(ValueError, match="GPU tensors"):
         kernels.quantize_rows(torch.zeros(2, 8, dtype=torch.bfloat16))
+    with pytest.raises(RuntimeError, match="not supported"):
+        kernels._gated_residual(torch.zeros(1, 2, 8), torch.zeros(1, 2, 8, dtype=torch.bfloat16),
+                                torch.zeros(1, 48, dtype=torch.bfloat16), torch.zeros(2), 2)
     with pytest.raises(ValueError, match="int32"):
         kernels.int8_epilogue(torch.zeros(2, 2), torch.ones(2), torch.ones(2), None)
     norm = types.SimpleNamespace(weight=torch.ones(8, dtype=torch.float32), eps=1e-6)
-    with pytest.raises(ValueError, match="GPU tensors|bfloat16"):
+    with pytest.raises((ValueError, RuntimeError), match="GPU tensors|not supported"):
         kernels._rms_adaln(torch.zeros(1, 2, 8, dtype=torch.bfloat16), norm,
                            torch.zeros(1, 48, dtype=torch.bfloat16), torch.zeros(2), 0, 1)
 
