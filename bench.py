@@ -765,14 +765,25 @@ def _cpu_name():
 
 
 CEILING_SOURCE = r"""
-// The GEMM's MFMA stream with no memory traffic: each wave holds 8 activation
-// and 16 weight fragments (bit patterns of real operands, read once) and 128
-// accumulators, and issues one k-step's 64 v_mfma_i32_16x16x64_i8 per
-// iteration in the GEMM's order, two waves per SIMD.
+// The GEMM's MFMA stream without DMA traffic, in five forms (a probe compiled
+// by bench.py, not part of the library). Fragments hold the bit patterns of
+// real operands (read once), since the clock under the power limit follows
+// their bit activity.
+//  kind 0  v_mfma_i32_16x16x64_i8 from registers: the shipped 8-wave tile's
+//          k-step (128x64 per wave, 128 accumulators, two waves per SIMD)
+//  kind 1  v_mfma_i32_32x32x32_i8 from registers, same work per k-step
+//          (4x2 tiles of 32x32: 128 accumulators, 24 fragments)
+//  kind 2  kind 0 with its fragments read from LDS, 0.375 reads per MFMA
+//          (12 reads per 32 MFMAs, double-buffered halves)
+//  kind 3  one wave per SIMD, 128x128 per wave, 256 accumulators in AGPRs
+//          (inline assembly), fragments from LDS at 0.25 reads per MFMA
+//  kind 4  kind 3 without the LDS reads
 #include <hip/hip_runtime.h>
 typedef int v4i __attribute__((ext_vector_type(4)));
-__global__ __launch_bounds__(512) void mfma_ceiling(const v4i* __restrict__ fa,
-                                                    const v4i* __restrict__ fw, int iters, int* out) {
+typedef int v16i __attribute__((ext_vector_type(16)));
+
+__global__ __launch_bounds__(512) void mfma16(const v4i* __restrict__ fa, const v4i* __restrict__ fw,
+                                              int iters, int* out) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int set = (blockIdx.x * 8 + wave) % 64;
   v4i a[8], w[16];
@@ -801,22 +812,172 @@ __global__ __launch_bounds__(512) void mfma_ceiling(const v4i* __restrict__ fa,
     for (int j = 0; j < 8; ++j) s ^= acc[i][j].x ^ acc[i][j].y ^ acc[i][j].z ^ acc[i][j].w;
   out[blockIdx.x * 512 + threadIdx.x] = s;
 }
-extern "C" int ceiling_launch(const void* fa, const void* fw, int iters, void* out, int blocks, void* stream) {
-  hipLaunchKernelGGL(mfma_ceiling, dim3(blocks), dim3(512), 0, (hipStream_t)stream, (const v4i*)fa,
-                     (const v4i*)fw, iters, (int*)out);
+
+__global__ __launch_bounds__(512) void mfma32(const v4i* __restrict__ fa, const v4i* __restrict__ fw,
+                                              int iters, int* out) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int set = (blockIdx.x * 8 + wave) % 64;
+  v4i a[16], w[8];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) a[i] = fa[((set * 16 + i) % 512) * 64 + lane];  // 512 KB of A fragments
+#pragma unroll
+  for (int j = 0; j < 8; ++j) w[j] = fw[(set * 8 + j) * 64 + lane];
+  v16i acc[4][2];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) acc[i][j] = v16i{};
+  for (int it = 0; it < iters; ++it) {
+#pragma unroll
+    for (int h = 0; h < 4; ++h)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_i32_32x32x32_i8(w[2 * h + j], a[4 * h + i], acc[i][j], 0, 0, 0);
+  }
+  int s = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) s ^= acc[i][j][e];
+  out[blockIdx.x * 512 + threadIdx.x] = s;
+}
+
+// 64 A fragments then 64 W fragments in LDS (1 KB each, lane-major).
+__device__ __forceinline__ void fill_lds(char* smem, const v4i* fa, const v4i* fw) {
+  for (int i = threadIdx.x; i < 64 * 64; i += blockDim.x) {
+    reinterpret_cast<v4i*>(smem)[i] = fa[i];
+    reinterpret_cast<v4i*>(smem + 65536)[i] = fw[i];
+  }
+  __syncthreads();
+}
+__device__ __forceinline__ v4i ldsfrag(const char* smem, int region, int f, int lane) {
+  return *reinterpret_cast<const v4i*>(smem + region * 65536 + (f & 63) * 1024 + lane * 16);
+}
+
+__global__ __launch_bounds__(512) void mfma16_lds(const v4i* __restrict__ fa, const v4i* __restrict__ fw,
+                                                  int iters, int* out) {
+  __shared__ __attribute__((aligned(1024))) char smem[131072];
+  fill_lds(smem, fa, fw);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  v4i a0[8], w0[4], a1[8], w1[4];
+  v4i acc[8][4];
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[i][j] = v4i{0, 0, 0, 0};
+  int f = wave * 8;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) a0[i] = ldsfrag(smem, 0, f + i, lane);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) w0[j] = ldsfrag(smem, 1, f + j, lane);
+  for (int it = 0; it < iters; ++it) {
+    f += 12;
+#pragma unroll
+    for (int t = 0; t < 32; ++t) {
+      acc[t / 4][t % 4] = __builtin_amdgcn_mfma_i32_16x16x64_i8(w0[t % 4], a0[t / 4], acc[t / 4][t % 4], 0, 0, 0);
+      if (t % 3 == 0 && t / 3 < 8) a1[t / 3] = ldsfrag(smem, 0, f + t / 3, lane);
+      if (t % 3 == 1 && t / 3 < 4) w1[t / 3] = ldsfrag(smem, 1, f + t / 3, lane);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    f += 12;
+#pragma unroll
+    for (int t = 0; t < 32; ++t) {
+      acc[t / 4][t % 4] = __builtin_amdgcn_mfma_i32_16x16x64_i8(w1[t % 4], a1[t / 4], acc[t / 4][t % 4], 0, 0, 0);
+      if (t % 3 == 0 && t / 3 < 8) a0[t / 3] = ldsfrag(smem, 0, f + t / 3, lane);
+      if (t % 3 == 1 && t / 3 < 4) w0[t / 3] = ldsfrag(smem, 1, f + t / 3, lane);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+  int s = 0;
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) s ^= acc[i][j].x ^ acc[i][j].y ^ acc[i][j].z ^ acc[i][j].w;
+  out[blockIdx.x * 512 + threadIdx.x] = s;
+}
+
+#define MFMA_AGPR(acc, w, a) asm volatile("v_mfma_i32_16x16x64_i8 %0, %1, %2, %0" : "+a"(acc) : "v"(w), "v"(a))
+
+template <bool READS>
+__global__ __launch_bounds__(256) void mfma16_agpr(const v4i* __restrict__ fa, const v4i* __restrict__ fw,
+                                                   int iters, int* out) {
+  __shared__ __attribute__((aligned(1024))) char smem[131072];
+  fill_lds(smem, fa, fw);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  v4i a0[8], w0[8], a1[8], w1[8];
+  v4i acc[8][8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[i][j] = v4i{0, 0, 0, 0};
+  int f = wave * 8;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) { a0[i] = ldsfrag(smem, 0, f + i, lane); a1[i] = ldsfrag(smem, 0, f + 8 + i, lane); }
+#pragma unroll
+  for (int j = 0; j < 8; ++j) { w0[j] = ldsfrag(smem, 1, f + j, lane); w1[j] = ldsfrag(smem, 1, f + 8 + j, lane); }
+  for (int it = 0; it < iters; ++it) {
+    f += 16;
+#pragma unroll
+    for (int t = 0; t < 64; ++t) {
+      MFMA_AGPR(acc[t / 8][t % 8], w0[t % 8], a0[t / 8]);
+      if (READS && t % 4 == 0) a1[t / 8] = ldsfrag(smem, 0, f + t / 8, lane);
+      if (READS && t % 4 == 2) w1[t / 8] = ldsfrag(smem, 1, f + t / 8, lane);
+    }
+    f += 16;
+#pragma unroll
+    for (int t = 0; t < 64; ++t) {
+      MFMA_AGPR(acc[t / 8][t % 8], w1[t % 8], a1[t / 8]);
+      if (READS && t % 4 == 0) a0[t / 8] = ldsfrag(smem, 0, f + t / 8, lane);
+      if (READS && t % 4 == 2) w0[t / 8] = ldsfrag(smem, 1, f + t / 8, lane);
+    }
+  }
+  asm volatile("s_nop 15\n s_nop 15" ::: "memory");
+  int s = 0;
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) s ^= acc[i][j].x ^ acc[i][j].y ^ acc[i][j].z ^ acc[i][j].w;
+  out[blockIdx.x * 256 + threadIdx.x] = s;
+}
+
+extern "C" int ceiling_launch(int kind, const void* fa, const void* fw, int iters, void* out, int blocks,
+                              void* stream) {
+  hipStream_t st = (hipStream_t)stream;
+  const v4i* A = (const v4i*)fa;
+  const v4i* W = (const v4i*)fw;
+  int* o = (int*)out;
+  switch (kind) {
+    case 0: hipLaunchKernelGGL(mfma16, dim3(blocks), dim3(512), 0, st, A, W, iters, o); break;
+    case 1: hipLaunchKernelGGL(mfma32, dim3(blocks), dim3(512), 0, st, A, W, iters, o); break;
+    case 2: hipLaunchKernelGGL(mfma16_lds, dim3(blocks), dim3(512), 0, st, A, W, iters, o); break;
+    case 3: hipLaunchKernelGGL(mfma16_agpr<true>, dim3(blocks), dim3(256), 0, st, A, W, iters, o); break;
+    default: hipLaunchKernelGGL(mfma16_agpr<false>, dim3(blocks), dim3(256), 0, st, A, W, iters, o); break;
+  }
   return (int)hipGetLastError();
 }
 """
 
+# kind -> (label, waves per block, MFMAs per wave per iteration, int-ops per MFMA)
+CEILING_KINDS = {
+    0: ("mfma16_regs", 8, 64, 2 * 16 * 16 * 64),
+    1: ("mfma32_regs", 8, 32, 2 * 32 * 32 * 32),
+    2: ("mfma16_lds_reads_0.375", 8, 64, 2 * 16 * 16 * 64),
+    3: ("mfma16_agpr_1wave_lds_reads_0.25", 4, 128, 2 * 16 * 16 * 64),
+    4: ("mfma16_agpr_1wave_regs", 4, 128, 2 * 16 * 16 * 64),
+}
+
 
 def run_ceiling(args):
-    """The chip's INT8 MFMA rate with no memory traffic: the GEMM's k-step MFMA
-    stream (two waves per SIMD, 128 accumulators each) from registers, with the
-    operands' bit patterns taken from the bench's own quantized activations and
-    int8 weights, from all-zero operands and from uniform random int8. The probe
-    is compiled here with hipcc (it is not part of the library). Under the power
-    limit the clock follows the operands' bit activity; the GEMM's fraction of
-    this rate is the share its memory traffic leaves."""
+    """The chip's INT8 MFMA rate without DMA traffic (CEILING_SOURCE, compiled
+    here with hipcc; not part of the library). Every form runs on the bench's
+    own quantized activations against uniform int8 weights, the shipped
+    16x16x64 register form also on all-zero and uniform random operands: under
+    the power limit the clock follows the operands' bit activity and the
+    register and LDS traffic per MFMA."""
     import ctypes
     import subprocess
     import tempfile
@@ -829,8 +990,8 @@ def run_ceiling(args):
                     "-amdgpu-mfma-vgpr-form", "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
                     src, "-o", lib], check=True, capture_output=True)
     probe = ctypes.CDLL(lib)
-    probe.ceiling_launch.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p,
-                                     ctypes.c_int, ctypes.c_void_p]
+    probe.ceiling_launch.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int,
+                                     ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p]
     g = torch.Generator().manual_seed(20261201 + CONFIG_INDEX)
     x = torch.randn(4096, 128, generator=g)
     x[:, torch.randperm(128, generator=g)[:2]] *= 20
@@ -843,13 +1004,14 @@ def run_ceiling(args):
     }
     blocks, iters = 1024, 400
     out = torch.empty(blocks * 512, dtype=torch.int32, device="cuda")
-    ops = blocks * 8 * iters * 64 * 2 * 16 * 16 * 64
-    res = {}
-    for name, (a, w) in sources.items():
+
+    def measure(kind, a, w):
+        _, waves, mfmas, opm = CEILING_KINDS[kind]
+        ops = blocks * waves * iters * mfmas * opm
         fa, fw = a.contiguous().cuda(), w.contiguous().cuda()   # 512 KB and 1 MB of fragments
-        launch = lambda: probe.ceiling_launch(fa.data_ptr(), fw.data_ptr(), iters, out.data_ptr(), blocks,
-                                             torch.cuda.current_stream().cuda_stream)
-        for _ in range(3):
+        launch = lambda: probe.ceiling_launch(kind, fa.data_ptr(), fw.data_ptr(), iters, out.data_ptr(),
+                                             blocks, torch.cuda.current_stream().cuda_stream)
+        for _ in range(5):  # the clock settles under the load first
             assert launch() == 0
         torch.cuda.synchronize()
         times = []
@@ -861,12 +1023,20 @@ def run_ceiling(args):
             e1.synchronize()
             times.append(e0.elapsed_time(e1) * 1e3)
         us = statistics.median(times)
-        res[name] = {"us": round(us, 1), "tops": round(ops / (us * 1e-6) / 1e12, 1),
-                     "frac_peak": round(ops / (us * 1e-6) / 1e12 / PEAK_INT8_TOPS, 4)}
-    return _side_line("INT8 MFMA ceiling without memory traffic (TOPS)", res["bench_operands"]["tops"],
-                      "TOPS", args, "MFMA stream from registers (GEMM k-step order)", res, dtype="int8",
-                      config={"blocks": blocks, "waves_per_block": 8, "iterations": iters,
-                              "mfma": "v_mfma_i32_16x16x64_i8"})
+        return {"us": round(us, 1), "tops": round(ops / (us * 1e-6) / 1e12, 1),
+                "frac_peak": round(ops / (us * 1e-6) / 1e12 / PEAK_INT8_TOPS, 4)}
+
+    res = {}
+    for kind, (label, *_rest) in CEILING_KINDS.items():
+        res[label] = measure(kind, *sources["bench_operands"])
+    for name in ("zeros", "uniform_random"):
+        res[f"mfma16_regs_{name}"] = measure(0, *sources[name])
+    # The first form measured runs before the clock has settled under load.
+    res["mfma16_regs_again"] = measure(0, *sources["bench_operands"])
+    return _side_line("INT8 MFMA ceiling without memory traffic (TOPS)", res["mfma16_regs_again"]["tops"],
+                      "TOPS", args, "MFMA stream from registers and LDS (GEMM k-step order)", res, dtype="int8",
+                      config={"blocks": blocks, "iterations": iters,
+                              "operands": "bench quantized activations x uniform int8 weights"})
 
 
 def main():

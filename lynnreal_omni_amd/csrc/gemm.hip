@@ -524,6 +524,9 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_fast(GemmArgs p) 
   const int wm = wave / WAVES_N, wn = wave % WAVES_N;
   const int64_t K = p.k;
   const int KT = kend - kbase;
+  // The k-step of K that k-step kt of this workgroup reads; DMAs issued past
+  // its last k-step re-read that one.
+  auto kpos = [&](int kt) { return kbase + (kt < KT ? kt : KT - 1); };
 
   const int64_t rows_a = min((int64_t)BM, p.m - m0);
   const int64_t rows_b = min((int64_t)BN, p.n - n0);
@@ -553,7 +556,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_fast(GemmArgs p) 
   auto dma_a = [&](int kt, int i) {
     if constexpr (KALIGNED) {
       dma16s(ra, a_ring + (kt % NA) * A_BYTES + a_block(wave, i) * 1024, a_off[i],
-             (uint32_t)((kbase + (kt < KT ? kt : KT - 1)) * BK));
+             (uint32_t)(kpos(kt) * BK));
       return;
     }
     const int64_t kbyte = (int64_t)(kbase + kt) * BK;
@@ -563,7 +566,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_fast(GemmArgs p) 
   auto dma_b = [&](int kt, int j) {
     if constexpr (KALIGNED) {
       dma16s(rb, b_ring + (kt % NB) * B_BYTES + b_block(wave, j) * 1024, b_off[j],
-             (uint32_t)((kbase + (kt < KT ? kt : KT - 1)) * BK));
+             (uint32_t)(kpos(kt) * BK));
       return;
     }
     const int64_t kbyte = (int64_t)(kbase + kt) * BK;
@@ -633,13 +636,13 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_fast(GemmArgs p) 
     // DMAs past the last k-step re-read the last one (every address stays in
     // the panel) into slots that no k-step reads again.
     auto pdma_a = [&](int kt) {
-      const uint32_t soff = (uint32_t)((kbase + (kt < KT ? kt : KT - 1)) * BK);
+      const uint32_t soff = (uint32_t)(kpos(kt) * BK);
 #pragma unroll
       for (int i = 0; i < PA; ++i)
         dma16s(ra, a_ring + (kt % NA) * A_BYTES + (q * PA + i) * 1024, pa_off[i], soff);
     };
     auto pdma_b = [&](int kt) {
-      const uint32_t soff = (uint32_t)((kbase + (kt < KT ? kt : KT - 1)) * BK);
+      const uint32_t soff = (uint32_t)(kpos(kt) * BK);
 #pragma unroll
       for (int j = 0; j < PB; ++j)
         dma16s(rb, b_ring + (kt % NB) * B_BYTES + (q * PB + j) * 1024, pb_off[j], soff);
