@@ -13,5 +13,6 @@ never as the thing measured or shipped. The product path
                      pin the C one, and the CPU baseline of bench.py
   oracle.bf16        bfloat16 <-> float32 conversions on numpy arrays
 
-Parity status of each function is listed in oracle/README.md.
+The checks that pin each function (golden fixtures, closed forms, torch's
+own library routines, brute force on small inputs) are in tests/test_oracle.py.
 """
