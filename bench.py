@@ -58,7 +58,7 @@ def parse():
                    help="tokens of the chain timed on the CPU (default: all of them, the whole config)")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--workload", choices=("c3", "c1", "c4", "c5", "rows", "qk", "flash", "adaln", "ceiling",
-                                          "shapes"),
+                                          "shapes", "splitk"),
                    default="c3",
                    help="c3: the projection chain (default, the headline line); c1: one W8A8 linear "
                         "(2048x5120 -> 5120) with the CPU torch path beside it; c4: the T=65536 W8A8 FFN "
@@ -67,7 +67,9 @@ def parse():
                         "C2/C3 shape; qk: QK RMSNorm + RoPE; flash: Flash token selection; adaln: the "
                         "adaLN table projection; ceiling: the GEMM's MFMA stream alone, from registers "
                         "(the power-limited INT8 ceiling, no memory traffic); shapes: the Flash "
-                        "model's four GEMM shapes at full M (D=5376), every large tile and hipBLASLt")
+                        "model's four GEMM shapes at full M (D=5376), every large tile and hipBLASLt; splitk: "
+                        "the split-K sweep behind the automatic schedule (M = 256 projections over tiles and "
+                        "K slices) and the out-proj shape with its last rows split along K")
     p.add_argument("--flush", action="store_true",
                    help="rows workload: overwrite the MALL before each launch and time launches one by one")
     p.add_argument("--no-vendor-gemm", dest="vendor_gemm", action="store_false",
@@ -425,6 +427,60 @@ def _eager_calls(fn, calls=400):
     t2 = time.perf_counter()
     return {"host_us_per_call": round((t1 - t0) / calls * 1e6, 2),
             "wall_us_per_call": round((t2 - t0) / calls * 1e6, 2), "calls": calls}
+
+
+def run_splitk(args):
+    """The split-K sweep behind the automatic schedule, device time per call of
+    graph-replayed launches (bf16 epilogue + bias, quantized N(0,1) activations
+    with 1% outlier channels x20): the M = 256 projections of config 5 (K = 5120,
+    N = 5120 and 20480) and the FFN-down shape at M = 256 (K = 20480) over the
+    small-M and 256x256 tiles in 1, 2, 4 and 8 K slices; and the out-proj shape
+    (12288 x 5120 x 5120) whole against its first 9728 rows plus its last 2560
+    rows split along K. Every split output is checked equal to the unsplit one."""
+    import torch
+    from lynnreal_omni_amd import kernels as k
+    from lynnreal_omni_amd.int8_gemm import int8_matmul
+
+    g = torch.Generator().manual_seed(20261201 + 4)
+
+    def operands(m, kk, n):
+        x = torch.randn(m, kk, generator=g)
+        x[:, torch.randperm(kk, generator=g)[: max(1, kk // 100)]] *= 20
+        q, s = k.quantize_rows(x.bfloat16().cuda())
+        w = torch.randint(-127, 128, (n, kk), dtype=torch.int8, generator=g).cuda()
+        cs = (torch.rand(n, generator=g) * 4e-3 + 1e-3).cuda()
+        b = (0.02 * torch.randn(n, generator=g)).bfloat16().cuda()
+        return q, s, w.t(), cs, b
+
+    out = {}
+    for m, kk, n in ((256, 5120, 5120), (256, 5120, 20480), (256, 20480, 5120)):
+        q, s, w, cs, b = operands(m, kk, n)
+        want = int8_matmul(q, w, s, cs, b)
+        row = {}
+        for tile in ((64, 80), (128, 160), (256, 80), (128, 128), (256, 256)):
+            for splits in (1, 2, 4, 8):
+                y = int8_matmul(q, w, s, cs, b, tile=tile, splits=splits)
+                assert torch.equal(y, want), (m, kk, n, tile, splits)
+                row[f"{tile[0]}x{tile[1]}_s{splits}"] = round(_event_time(
+                    lambda: int8_matmul(q, w, s, cs, b, tile=tile, splits=splits), 20), 2)
+        # the automatic schedule last, with the clock settled under the load
+        row["auto"] = round(_event_time(lambda: int8_matmul(q, w, s, cs, b), 20), 2)
+        out[f"m{m}_k{kk}_n{n}"] = row
+    m, kk, n, cut = 12288, 5120, 5120, 9728
+    q, s, w, cs, b = operands(m, kk, n)
+    want = int8_matmul(q, w, s, cs, b)
+    tail = {}
+    for splits in (1, 2, 4, 8):
+        def hybrid():
+            return (int8_matmul(q[:cut], w, s[:cut], cs, b),
+                    int8_matmul(q[cut:], w, s[cut:], cs, b, tile=(256, 256), splits=splits))
+        assert torch.equal(torch.cat(hybrid()), want)
+        tail[f"first_{cut}_rows_then_last_split_{splits}"] = round(_event_time(hybrid, 10), 1)
+    tail["whole"] = round(_event_time(lambda: int8_matmul(q, w, s, cs, b), 10), 1)
+    out["out_proj_tail"] = tail
+    return _side_line("split-K sweep (us per call)", out["m256_k20480_n5120"]["auto"], "us", args,
+                      "split-K schedule sweep", out, dtype="int8", higher_is_better=False,
+                      timing="HIP graph of back-to-back calls, median of 5 replays")
 
 
 def run_c4(args):
@@ -1059,6 +1115,7 @@ def main():
         print(json.dumps(run_c5(args)), flush=True)
         return 0
     side = {"rows": run_rows, "qk": run_qk, "flash": run_flash, "adaln": run_adaln, "ceiling": run_ceiling,
+            "splitk": run_splitk,
             "shapes": run_shapes}
     if args.workload in side:
         log(f"device {torch.cuda.get_device_name(0)}; workload {args.workload}")
