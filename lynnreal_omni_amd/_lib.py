@@ -168,20 +168,25 @@ def ptr(t: torch.Tensor | None) -> int | None:
 
 
 _workspaces: dict[tuple[int, int], torch.Tensor] = {}
+_MAX_WORKSPACES = 16
 
 
 def workspace(t: torch.Tensor, nbytes: int) -> tuple[int | None, int]:
     """(pointer, bytes) of a device workspace of at least `nbytes` for the
     caller's current stream on t's device, or (None, 0) when none is needed.
 
-    One buffer is kept per (device, stream) and grown on demand: kernels that
-    share it run in stream order, and torch's caching allocator reuses a
-    replaced buffer only behind the work already queued on that stream."""
+    One buffer is kept per (device, stream), grown on demand, for the 16
+    most recently used (device, stream) pairs: kernels that share a buffer
+    run in stream order, and torch's caching allocator hands a released
+    buffer's memory to a later allocation on the same stream only, behind
+    the work already queued there."""
     if nbytes <= 0:
         return None, 0
     key = (t.get_device(), stream(t))
-    buf = _workspaces.get(key)
+    buf = _workspaces.pop(key, None)
     if buf is None or buf.numel() < nbytes:
         buf = torch.empty(nbytes, dtype=torch.uint8, device=t.device)
-        _workspaces[key] = buf
+    _workspaces[key] = buf  # most recent last
+    while len(_workspaces) > _MAX_WORKSPACES:
+        _workspaces.pop(next(iter(_workspaces)))
     return buf.data_ptr(), buf.numel()

@@ -18,6 +18,8 @@ Differences from the reference, by design:
 """
 from __future__ import annotations
 
+import functools
+
 import torch
 
 from . import _lib
@@ -82,17 +84,11 @@ def _launch(a, b, row_scale, column_scale, bias, out, epilogue, tile, residual=N
     return out
 
 
-_ws_sizes: dict[tuple, int] = {}
-
-
+@functools.lru_cache(maxsize=4096)
 def _workspace_bytes(m, n, k, splits, tile_id) -> int:
     """Workspace bytes of the library's split-K schedule for this shape (0
     when it does not split K), cached per shape."""
-    key = (m, n, k, splits, tile_id)
-    size = _ws_sizes.get(key)
-    if size is None:
-        size = _ws_sizes[key] = int(_lib.load().lr_int8_gemm_workspace_size(m, n, k, splits, tile_id))
-    return size
+    return int(_lib.load().lr_int8_gemm_workspace_size(m, n, k, splits, tile_id))
 
 
 def _f32_vector(t):
