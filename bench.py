@@ -599,7 +599,7 @@ def run_shapes(args):
     from lynnreal_omni_amd.int8_gemm import int8_matmul
     shapes = {"qkv": (16385, 21504, 5376), "out": (16385, 5376, 7168),
               "up": (49153, 28672, 5376), "down": (16385, 5376, 14336)}
-    tiles = [None, (256, 256), "256x256_w4x2", (256, 192), (256, 128), (128, 256), (128, 128)]
+    tiles = [None, (256, 256), "persistent", "256x256_w4x2", (256, 192), (256, 128), (128, 256), (128, 128)]
     g = torch.Generator(device="cuda").manual_seed(219)
     reps = max(args.steps // 4, 3)
     kernels, total_ops, total_us = {}, 0, 0.0

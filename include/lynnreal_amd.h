@@ -63,7 +63,8 @@ extern "C" {
 #define LR_TILE_128x160 11 /* 128x160, 4 waves of 64x80: weight streaming for M <= 256 */
 #define LR_TILE_192x256 12 /* 192x256, 8 waves of 96x64: fills the last wave of tiles at long K */
 #define LR_TILE_256x256_PERSISTENT 13 /* 256x256 on a persistent grid (one workgroup per CU looping
-                                        over the tiles); replaces model/int8_tma.py:12-41 */
+                                        over the tiles, each tile's last k-steps loading the next
+                                        tile's first ones); replaces model/int8_tma.py:12-41 */
 
 /* Library version; bumped whenever a signature below changes. */
 int lr_abi_version(void);

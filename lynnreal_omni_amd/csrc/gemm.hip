@@ -469,10 +469,7 @@ __device__ __forceinline__ void dma16s(__amdgpu_buffer_rsrc_t rsrc, void* lds, u
 // 16-byte bank groups; measured on gfx950 this runs ds_read_b128 at 94% of
 // the rate of a contiguous read (an extra (R / 8) % 2 term drops it to 71%).
 //
-// PERSIST: a grid of at most one workgroup per CU loops over the tiles in
-// launch order (pid = blockIdx.x, + gridDim.x, ...), the schedule of the
-// reference's persistent kernel (model/int8_tma.py:12-29); otherwise each
-// workgroup computes one tile.
+// Each workgroup computes one tile (gemm_stream is the persistent form).
 //
 // Split-K (p.splits = S > 1, one tile per workgroup, raw int32 epilogue):
 // workgroup g computes k-steps [s * KT / S, (s + 1) * KT / S) of tile g / S,
@@ -480,7 +477,7 @@ __device__ __forceinline__ void dma16s(__amdgpu_buffer_rsrc_t rsrc, void* lds, u
 // p.c (int32 [S, M, N]); splitk_reduce adds the slices (exact integer sums,
 // so any split gives the same int32 result) and applies the epilogue.
 template <int BM, int BN, int WAVES_M, int WAVES_N, int EPI, bool BIAS, int NA, int NB, bool KALIGNED,
-          bool PP, bool PERSIST = false>
+          bool PP>
 __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_fast(GemmArgs p) {
   constexpr int BK = 128;
   constexpr int NWAVES = WAVES_M * WAVES_N;
@@ -508,14 +505,13 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_fast(GemmArgs p) 
   char* const a_ring = smem;
   char* const b_ring = smem + NA * A_BYTES;
 
-  const int tiles = p.tiles_m * p.tiles_n;
   const int kt_all = (int)((p.k + BK - 1) / BK);
-  const int splits = PERSIST ? 1 : p.splits;
-  const int slice = PERSIST ? 0 : (int)blockIdx.x % splits;
+  const int splits = p.splits;
+  const int slice = (int)blockIdx.x % splits;
   // k-steps [kbase, kend) of the tile; no slice is empty when splits <= KT.
   const int kbase = slice * kt_all / splits, kend = (slice + 1) * kt_all / splits;
-  if (!PERSIST && p.splits > 1) p.c = static_cast<int32_t*>(p.c) + (int64_t)slice * p.m * p.n;
-  for (int pid = PERSIST ? (int)blockIdx.x : (int)blockIdx.x / p.splits;;) {
+  if (splits > 1) p.c = static_cast<int32_t*>(p.c) + (int64_t)slice * p.m * p.n;
+  const int pid = (int)blockIdx.x / splits;
   int tm, tn;
   tile_coords(p, pid, tm, tn);
   const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
@@ -845,13 +841,295 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_fast(GemmArgs p) 
   } else {
     store_tile<FM, FN, WM, WN, EPI, BIAS>(p, acc, m0, n0, wm, wn, lane);
   }
-  if constexpr (!PERSIST) break;
-  pid += gridDim.x;
-  if (pid >= tiles) break;
-  // Every wave is done with this tile's staging area before the next tile's
-  // DMAs refill the rings that share its LDS.
-  __syncthreads();
+}
+
+// ------------------------------------- persistent 256x256, streamed tiles ----
+// The persistent form of the 256x256 GEMM behind int8_tma.matmul: a grid of
+// at most one workgroup per CU loops over the tiles in launch order (pid =
+// blockIdx.x, + gridDim.x, ...), the schedule of the reference's persistent
+// kernel (model/int8_tma.py:12-29), with gemm_fast's ping-pong k-loop (2x4
+// wave grid). Its tiles follow each other without a cold start: the
+// two DMAs that a tile's last k-steps issue past its end, which the
+// one-tile-per-workgroup kernel spends re-reading its last k-step, load the
+// next tile's k-steps 0 and 1 instead, so the next tile's operands arrive
+// while this tile's outputs are written. The ring slots continue across
+// tiles (k-step g of the workgroup, counted over its tiles, lives in A slot
+// g % 3 and W slot g % 2). The epilogue then has only the A slot of the
+// tile's last k-step free (32 KB, 4 KB per wave), so it stages the 128x64
+// bf16 outputs of a wave in four passes of 32 rows (row pitch 128 bytes,
+// 16-byte chunks XOR-swizzled by row) instead of the whole tile at once.
+// K % 128 == 0 and K >= 256.
+
+// The pass-staged epilogue of one wave's 128x64 sub-tile (N % 8 == 0 and
+// 16-byte aligned outputs, as for store_tile_staged): pass p stages rows
+// 32p .. 32p + 31 (fragments 2p and 2p + 1) in the MFMA layout, then each lane
+// finishes and stores 4 whole 16-byte chunks of them.
+template <int EPI, bool BIAS>
+__device__ __forceinline__ void store_tile_passes(const GemmArgs& p, const v4i (&acc)[8][4], char* stage,
+                                                  int64_t m0, int64_t n0, int wm, int wn, int lane) {
+  constexpr int FM = 8, FN = 4, WM = 128, WN = 64;
+  const int lr_ = lane & 15, lg = lane >> 4;
+  float rsv[FM];
+  float4 csv[FN];
+  uint2 bv[FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i) {
+    const int64_t row = m0 + wm * WM + 16 * i + lr_;
+    rsv[i] = p.rs[row < p.m ? row : p.m - 1];
   }
+#pragma unroll
+  for (int j = 0; j < FN; ++j) {
+    const int64_t col = n0 + wn * WN + 16 * j + 4 * lg;
+    const int64_t c = col < p.n ? col : p.n - 4;  // N % 8 == 0 on this path
+    csv[j] = *reinterpret_cast<const float4*>(p.cs + c);
+    if (BIAS) bv[j] = *reinterpret_cast<const uint2*>(p.bias + c);
+  }
+  const bool seq_covers = p.sequence >= p.m;
+  // Unrolled: the accumulator indices must be constants, or the array would
+  // live in scratch memory.
+#pragma unroll
+  for (int pass = 0; pass < 4; ++pass) {
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+      float b0 = 0.f, b1 = 0.f, b2 = 0.f, b3 = 0.f;
+      if (BIAS) {
+        b0 = bf_lo(bv[j].x); b1 = bf_hi(bv[j].x); b2 = bf_lo(bv[j].y); b3 = bf_hi(bv[j].y);
+      }
+#pragma unroll
+      for (int ii = 0; ii < 2; ++ii) {
+        const int i = 2 * pass + ii;
+        const float v0 = dequant<BIAS>(acc[i][j][0], rsv[i], csv[j].x, b0);
+        const float v1 = dequant<BIAS>(acc[i][j][1], rsv[i], csv[j].y, b1);
+        const float v2 = dequant<BIAS>(acc[i][j][2], rsv[i], csv[j].z, b2);
+        const float v3 = dequant<BIAS>(acc[i][j][3], rsv[i], csv[j].w, b3);
+        const int r = 16 * ii + lr_;
+        const int chunk = (2 * j + (lg >> 1)) ^ (r & 7);
+        *reinterpret_cast<uint2*>(stage + r * 128 + chunk * 16 + (lg & 1) * 8) =
+            make_uint2(pack_bf2(v0, v1), pack_bf2(v2, v3));
+      }
+    }
+    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): this wave's staging writes are done
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+    // Gated: two chunks at a time (their residual and gate loads in flight
+    // together); four at once spill registers next to the accumulators.
+    constexpr int BATCH = EPI == EPI_GATED ? 2 : 4;
+#pragma unroll
+    for (int s0 = 0; s0 < 4; s0 += BATCH) {
+      uint4 v[BATCH], xv[BATCH], gv[BATCH];
+      int64_t o[BATCH];
+      bool ok[BATCH];
+#pragma unroll
+      for (int b = 0; b < BATCH; ++b) {
+        const int q = (s0 + b) * 64 + lane;
+        const int r = q >> 3, ch = q & 7;
+        const int64_t row = m0 + wm * WM + 32 * pass + r;
+        const int64_t col = n0 + wn * WN + ch * 8;
+        ok[b] = row < p.m && col < p.n;
+        o[b] = row * p.n + col;
+        v[b] = *reinterpret_cast<const uint4*>(stage + r * 128 + ((ch ^ (r & 7)) << 4));
+        if (EPI == EPI_GATED) {
+          // Clamped (always valid) addresses, so that no load sits under a branch.
+          const int64_t row_l = ok[b] ? row : m0, col_l = ok[b] ? col : n0;
+          const int64_t tr = clamp_index(
+              p.indices[row < p.m ? (seq_covers ? row : row % p.sequence) : 0], p.table_rows);
+          xv[b] = load_nt(reinterpret_cast<const uint4*>(p.resid + row_l * p.n + col_l));
+          gv[b] = *reinterpret_cast<const uint4*>(p.table + tr * p.table_width +
+                                                   (int64_t)p.gate_slot * p.n + col_l);
+        }
+      }
+#pragma unroll
+      for (int b = 0; b < BATCH; ++b) {
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          const uint32_t u = word_of(v[b], w);
+          uint32_t y = u;
+          if (EPI == EPI_GELU) {
+            y = pack_bf2(fast_gelu_tanh(bf_lo(u)), fast_gelu_tanh(bf_hi(u)));
+          } else if (EPI == EPI_GATED) {
+            const uint32_t x = word_of(xv[b], w), g = word_of(gv[b], w);
+            y = pack_bf2(bf_lo(x) + round_bf(bf_lo(g) * bf_lo(u)), bf_hi(x) + round_bf(bf_hi(g) * bf_hi(u)));
+          }
+          if (w == 0) v[b].x = y; else if (w == 1) v[b].y = y; else if (w == 2) v[b].z = y; else v[b].w = y;
+        }
+        if (ok[b]) store_c16(static_cast<uint16_t*>(p.c) + o[b], v[b]);
+      }
+    }
+    // This pass's chunks are in registers before the next pass overwrites them.
+    __builtin_amdgcn_s_waitcnt(0xc07f);
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
+template <int EPI, bool BIAS>
+__global__ __launch_bounds__(512) void gemm_stream(GemmArgs p) {
+  constexpr int BM = 256, BN = 256, BK = 128, NA = 3, NB = 2, WAVES_N = 4;
+  constexpr int WM = 128, WN = 64, FM = 8, FN = 4;
+  constexpr int A_BYTES = BM * BK, B_BYTES = BN * BK;
+  constexpr int PA = 8, PB = 8;  // 1 KB DMAs per wave per k-step
+  __shared__ __attribute__((aligned(1024))) char smem[NA * A_BYTES + NB * B_BYTES];
+  char* const a_ring = smem;
+  char* const b_ring = smem + NA * A_BYTES;
+
+  const int tiles = p.tiles_m * p.tiles_n;
+  const int64_t K = p.k;
+  const int KT = (int)(K / BK);
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int wm = wave / WAVES_N, wn = wave % WAVES_N;
+  const int grp = wave >> 2, q = wave & 3;
+  const int drow = lane >> 3;
+  const int dchunk = ((lane & 7) ^ drow) * 16;
+  uint32_t pa_off[PA], pb_off[PB];
+#pragma unroll
+  for (int i = 0; i < PA; ++i) pa_off[i] = (uint32_t)(((q * PA + i) * 8 + drow) * K + dchunk);
+#pragma unroll
+  for (int j = 0; j < PB; ++j) pb_off[j] = (uint32_t)(((q * PB + j) * 8 + drow) * K + dchunk);
+  const int r16 = lane & 15;
+  const int rd_key = r16 & 7;
+  const int rd_row = (r16 >> 3) * 1024 + (r16 & 7) * 128;
+  const int rd_slot0 = (((lane >> 4) + 0) ^ rd_key) * 16;
+  const int rd_slot1 = (((lane >> 4) + 4) ^ rd_key) * 16;
+  auto frag = [&](const char* base, int f, int h) -> v4i {
+    return *reinterpret_cast<const v4i*>(base + f * 2048 + rd_row + (h ? rd_slot1 : rd_slot0));
+  };
+  // Panel descriptors of tile pid (rows past M / N read as zero).
+  auto panel_a = [&](int pid) {
+    int tm, tn;
+    tile_coords(p, pid, tm, tn);
+    const int64_t m0 = (int64_t)tm * BM;
+    return __builtin_amdgcn_make_buffer_rsrc((void*)(p.a + m0 * K), (short)0,
+                                             (int)(min((int64_t)BM, p.m - m0) * K), 0x00020000);
+  };
+  auto panel_b = [&](int pid) {
+    int tm, tn;
+    tile_coords(p, pid, tm, tn);
+    const int64_t n0 = (int64_t)tn * BN;
+    return __builtin_amdgcn_make_buffer_rsrc((void*)(p.b + n0 * K), (short)0,
+                                             (int)(min((int64_t)BN, p.n - n0) * K), 0x00020000);
+  };
+  auto barrier = [&]() {
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  constexpr int kWaitA = 0x70 | 0xf00 | PA;  // vmcnt(PA): all but the newest k-step landed
+  constexpr int kWaitB = 0x70 | 0xf00 | PB;
+  constexpr int kWaitLds = 0xc07f;           // lgkmcnt(0)
+
+  int g = 0;  // the workgroup's k-steps before this tile (ring position)
+  for (int pid = blockIdx.x; pid < tiles; pid += gridDim.x, g += KT) {
+    int tm, tn;
+    tile_coords(p, pid, tm, tn);
+    const int64_t m0 = (int64_t)tm * BM, n0 = (int64_t)tn * BN;
+    const bool first = pid == (int)blockIdx.x;
+    const int next = pid + (int)gridDim.x;
+    const bool has_next = next < tiles;
+    const __amdgpu_buffer_rsrc_t ra = panel_a(pid), rb = panel_b(pid);
+    const __amdgpu_buffer_rsrc_t ra_n = has_next ? panel_a(next) : ra;
+    const __amdgpu_buffer_rsrc_t rb_n = has_next ? panel_b(next) : rb;
+    // k-step kt >= KT of this tile is k-step kt - KT of the next one, or past
+    // the last tile a re-read of this tile's last k-step.
+    auto pdma_a = [&](int kt) {
+      const bool nxt = kt >= KT && has_next;
+      const uint32_t soff = (uint32_t)((kt < KT ? kt : (nxt ? kt - KT : KT - 1)) * BK);
+      char* slot = a_ring + ((g + kt) % NA) * A_BYTES;
+#pragma unroll
+      for (int i = 0; i < PA; ++i) dma16s(nxt ? ra_n : ra, slot + (q * PA + i) * 1024, pa_off[i], soff);
+    };
+    auto pdma_b = [&](int kt) {
+      const bool nxt = kt >= KT && has_next;
+      const uint32_t soff = (uint32_t)((kt < KT ? kt : (nxt ? kt - KT : KT - 1)) * BK);
+      char* slot = b_ring + ((g + kt) % NB) * B_BYTES;
+#pragma unroll
+      for (int j = 0; j < PB; ++j) dma16s(nxt ? rb_n : rb, slot + (q * PB + j) * 1024, pb_off[j], soff);
+    };
+
+    v4i acc[FM][FN];
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; ++j) acc[i][j] = v4i{0, 0, 0, 0};
+    v4i a0[FM], w0[FN], a1[FM], w1[FN];
+    auto read_all = [&](int kt) {
+      const char* sa = a_ring + ((g + kt) % NA) * A_BYTES;
+      const char* sb = b_ring + ((g + kt) % NB) * B_BYTES;
+#pragma unroll
+      for (int i = 0; i < FM; ++i) a0[i] = frag(sa, wm * FM + i, 0);
+#pragma unroll
+      for (int j = 0; j < FN; ++j) w0[j] = frag(sb, wn * FN + j, 0);
+#pragma unroll
+      for (int i = 0; i < FM; ++i) a1[i] = frag(sa, wm * FM + i, 1);
+#pragma unroll
+      for (int j = 0; j < FN; ++j) w1[j] = frag(sb, wn * FN + j, 1);
+    };
+    auto compute = [&]() {
+#pragma unroll
+      for (int t = 0; t < FM * FN; ++t) {
+        const int i = t / FN, j = t % FN;
+        acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(w0[j], a0[i], acc[i][j], 0, 0, 0);
+      }
+#pragma unroll
+      for (int t = 0; t < FM * FN; ++t) {
+        const int i = t / FN, j = t % FN;
+        acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(w1[j], a1[i], acc[i][j], 0, 0, 0);
+      }
+    };
+    // The schedule of gemm_fast's ping-pong loop. A later tile's k-steps 0
+    // and 1 were issued by the tile before it, whose last waits (A(KT) and
+    // W(KT)) covered k-step 0; the first waits in the loop (all but the newest
+    // k-step landed) then also wait for the previous tile's output stores.
+    if (grp == 0) {
+      if (first) {
+        pdma_a(0);
+        pdma_a(1);
+        __builtin_amdgcn_s_waitcnt(kWaitA);
+      }
+      barrier();
+      for (int kt = 0; kt < KT; ++kt) {
+        read_all(kt);  // phase 2kt
+        pdma_a(kt + 2);
+        __builtin_amdgcn_s_waitcnt(kWaitLds);
+        barrier();
+        compute();  // phase 2kt + 1
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_waitcnt(kWaitA);
+        barrier();
+      }
+      barrier();  // phase 2KT: group 1 computes the last k-step
+    } else {
+      if (first) {
+        pdma_b(0);
+        pdma_b(1);
+        __builtin_amdgcn_s_waitcnt(kWaitB);
+      }
+      barrier();
+      barrier();  // phase 0: group 0 reads k-step 0
+      for (int kt = 0; kt < KT; ++kt) {
+        read_all(kt);  // phase 2kt + 1
+        // With four waves across N this wave alone in its group reads the W
+        // rows it refills.
+        __builtin_amdgcn_s_waitcnt(kWaitLds);
+        pdma_b(kt + 2);
+        __builtin_amdgcn_s_waitcnt(kWaitB);  // W(kt + 1) landed
+        barrier();
+        compute();  // phase 2kt + 2
+        barrier();
+      }
+    }
+    // Every wave has read k-step KT - 1, so its A slot is free for the
+    // epilogue; the slots of the next tile's k-steps 0 and 1 stay untouched.
+    // The next tile's first barrier keeps its A(2) DMA, which refills this
+    // slot, behind every wave's epilogue.
+    char* const stage = a_ring + ((g + KT - 1) % NA) * A_BYTES + wave * 4096;
+    if (EPI != EPI_RAW && p.staged)
+      store_tile_passes<EPI, BIAS>(p, acc, stage, m0, n0, wm, wn, lane);
+    else
+      store_tile<FM, FN, WM, WN, EPI, BIAS>(p, acc, m0, n0, wm, wn, lane);
+  }
+  // The last tile's trailing DMAs land before the workgroup's LDS is freed.
+  __builtin_amdgcn_s_waitcnt(0x70 | 0xf00);  // vmcnt(0)
 }
 
 // -------------------------------------------------------- generic GEMM ----
@@ -969,11 +1247,12 @@ void launch_fast_cfg(GemmArgs& p, hipStream_t st) {
                        dim3(grid), dim3(64 * WAVES_M * WAVES_N), 0, st, p);
 }
 
-// The persistent 256x256 block (K % 128 == 0, else one tile per workgroup):
-// one workgroup per CU, rounded down to a multiple of the 8 XCDs.
+// The persistent 256x256 block, streamed (K % 128 == 0 and K >= 256, else one
+// tile per workgroup): one workgroup per CU, rounded down to a multiple of the
+// 8 XCDs (so blockIdx % 8 is the XCD, as the tile order assumes).
 template <int EPI, bool BIAS>
 void launch_persistent(GemmArgs& p, hipStream_t st) {
-  if (p.k % 128 != 0) {
+  if (p.k % 128 != 0 || p.k < 256) {
     launch_fast_cfg<256, 256, 2, 4, EPI, BIAS>(p, st);
     return;
   }
@@ -981,10 +1260,8 @@ void launch_persistent(GemmArgs& p, hipStream_t st) {
   p.tiles_n = (int)((p.n + 255) / 256);
   const int64_t tiles = (int64_t)p.tiles_m * p.tiles_n;
   const int64_t cus = compute_units() >= 8 ? compute_units() / 8 * 8 : 8;
-  const unsigned grid = (unsigned)(tiles < cus ? tiles : cus);
-  hipLaunchKernelGGL((gemm_fast<256, 256, 2, 4, EPI, BIAS, GEMM_RING_A, GEMM_RING_B, true,
-                                GEMM_PINGPONG && GEMM_RING_A == 3 && GEMM_RING_B == 2, true>),
-                     dim3(grid), dim3(512), 0, st, p);
+  hipLaunchKernelGGL((gemm_stream<EPI, BIAS>), dim3((unsigned)(tiles < cus ? tiles : cus)), dim3(512), 0, st,
+                     p);
 }
 
 template <int EPI, bool BIAS>
@@ -1167,14 +1444,25 @@ struct Plan {
   int splits;
 };
 
-// The fast-path schedule: the tile (LR_TILE_AUTO: by shape) and the split-K
-// factor (splits 0: by shape when a workspace is allowed, else 1).
-Plan plan(int64_t m, int64_t n, int64_t k, int tile, int splits, bool workspace) {
+// The fast-path schedule: the tile (LR_TILE_AUTO: by shape and epilogue) and
+// the split-K factor (splits 0: by shape when a workspace is allowed, else 1).
+// Where the shape takes 256x256 tiles over at least two waves of the chip and
+// the epilogue is bf16 or GELU, the persistent grid with streamed tiles runs
+// 1-2% faster than one tile per workgroup (QKV 12288x15360x5120: 660 against
+// 672 us, FFN-up 894 against 902-914 us, the Flash model's QKV and out-proj
+// shapes at full M likewise; same box). Its pass-staged gated epilogue is
+// slower (out-proj 286 against 265 us), so the gated and raw epilogues keep
+// one tile per workgroup.
+Plan plan(int64_t m, int64_t n, int64_t k, int tile, int splits, bool workspace, int epilogue) {
   Plan pl{tile == LR_TILE_AUTO ? auto_tile(m, n, k) : tile, splits > 0 ? splits : 1};
   if (splits == 0 && workspace && tile == LR_TILE_AUTO) {
     const int s = auto_splits(m, n, k);
     if (s > 1) pl = Plan{LR_TILE_128x160, s};
   }
+  if (tile == LR_TILE_AUTO && pl.tile == LR_TILE_256x256 && pl.splits == 1 &&
+      (epilogue == LR_EPI_BF16 || epilogue == LR_EPI_GELU_TANH) && k % 128 == 0 && k >= 256 &&
+      ((m + 255) / 256) * ((n + 255) / 256) >= 2 * (int64_t)compute_units())
+    pl.tile = LR_TILE_256x256_PERSISTENT;
   return pl;
 }
 
@@ -1228,7 +1516,7 @@ int gemm_impl(const int8_t* a, const int8_t* b, int64_t b_stride_k, int64_t b_st
     LR_REQUIRE((m + 63) / 64 <= 65535, "int8_gemm: generic path supports M <= 4194240");
     LR_REQUIRE(splits <= 1, "int8_gemm: split-K needs the MFMA fast path");
   } else {
-    const Plan pl = plan(m, n, k, tile, splits, workspace != nullptr);
+    const Plan pl = plan(m, n, k, tile, splits, workspace != nullptr, epilogue);
     tile = pl.tile;
     const int64_t tiles = ((m + tile_rows(tile) - 1) / tile_rows(tile)) *
                           ((n + tile_cols(tile) - 1) / tile_cols(tile));
@@ -1369,5 +1657,5 @@ extern "C" int64_t lr_int8_gemm_workspace_size(int64_t m, int64_t n, int64_t k, 
   if (m <= 0 || n <= 0 || k <= 0 || k % 128 != 0 || n % 4 != 0 || splits < 0 || splits > 64 ||
       tile < LR_TILE_AUTO || tile > LR_TILE_256x256_PERSISTENT || tile == LR_TILE_GENERIC)
     return 0;
-  return split_workspace(m, n, plan(m, n, k, tile, splits, true).splits);
+  return split_workspace(m, n, plan(m, n, k, tile, splits, true, LR_EPI_RAW_INT32).splits);
 }
