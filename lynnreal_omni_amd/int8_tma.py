@@ -10,9 +10,9 @@ with the same ping-pong k-loop and whole-line global->LDS DMAs, so the output
 is bit for bit int8_matmul's. Where the async TMA loads let the reference's
 next tile start early, here a tile's last k-steps already load the next
 tile's first two k-steps into the LDS rings, and the epilogue stages its
-outputs through the one ring slot left free. int8_matmul keeps one tile per
-workgroup for every M: the persistent grid measured level with it (within
-about 1% either way by shape).
+outputs through the one ring slot left free. int8_matmul takes the same
+kernel by itself for 256x256 launches of at least two waves of tiles with the
+bf16 or GELU epilogue, and one tile per workgroup otherwise.
 """
 from __future__ import annotations
 
