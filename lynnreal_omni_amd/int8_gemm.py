@@ -6,10 +6,14 @@ against its torch path at script/precompile.py:55-64); `_torch_matmul` is the
 reference's torch path (model/int8_gemm.py:84-92).
 
 Differences from the reference, by design:
-  * There is no autotuner, tile cache or Triton. The kernel's tile is chosen
-    by shape inside the library; `tile=` accepts the reference's tile tuples
-    (BM, BN, BK, warps, stages[, group]) and maps (BM, BN) onto the HIP tile
-    of the same shape, or raises ValueError.
+  * No Triton. The kernel's tile is chosen by shape inside the library;
+    `tile=` accepts the reference's tile tuples (BM, BN, BK, warps, stages[,
+    group]) and maps (BM, BN) onto the HIP tile of the same shape, or raises
+    ValueError. With LYNNREAL_AMD_AUTOTUNE=1 the first call of each shape
+    times every HIP tile instead and keeps the fastest in memory and in a JSON
+    file keyed by library, device and shape (the reference's autotuner and
+    tile cache, model/int8_gemm.py:53-81,124-151); every tile computes the
+    same bits, so the choice only changes the time.
   * A kernel failure raises instead of silently falling back to torch._int_mm:
     the HIP path is the product, a hidden fallback would mask it.
   * New keyword-only epilogues: activation="gelu_tanh" (GELU-tanh on the bf16
@@ -19,6 +23,10 @@ Differences from the reference, by design:
 from __future__ import annotations
 
 import functools
+import hashlib
+import json
+import os
+import pathlib
 
 import torch
 
@@ -39,7 +47,7 @@ _TILES = {
 
 
 def _tile_id(tile) -> int:
-    if tile is None:
+    if tile is None or tile == "auto":
         return _lib.TILE_AUTO
     if isinstance(tile, str):
         named = {"generic": _lib.TILE_GENERIC, "256x256_w4x2": _lib.TILE_256x256_W4x2,
@@ -74,6 +82,9 @@ def _launch(a, b, row_scale, column_scale, bias, out, epilogue, tile, residual=N
     if table is not None:
         table_width = table.shape[-1]
         table_rows = table.numel() // table_width
+    if tile is None and splits is None and _autotune_enabled():
+        tile = _tuned_tile(a, b, row_scale, column_scale, bias, out, epilogue, residual, table,
+                           indices, sequence, gate_slot)
     tile_id = _tile_id(tile)
     splits = 0 if splits is None else int(splits)
     ws, ws_bytes = _lib.workspace(a, _workspace_bytes(m, n, k, splits, tile_id))
@@ -82,6 +93,107 @@ def _launch(a, b, row_scale, column_scale, bias, out, epilogue, tile, residual=N
               epilogue, _lib.ptr(residual), _lib.ptr(table), table_rows, table_width,
               _lib.ptr(indices), sequence, gate_slot, ws, ws_bytes, splits, tile_id, _lib.stream(a))
     return out
+
+
+# --------------------------------------------------------- autotuning ----
+# The candidates: every HIP tile, the library's own choice first, so that a
+# tie keeps it.
+_CANDIDATES = (None, (256, 256), "persistent", (192, 256), (256, 192), (256, 128), (128, 256),
+               (128, 128), (64, 128), (256, 80), (128, 160), (64, 80))
+_selected: dict[tuple, object] = {}
+_prefixes: dict[int, tuple] = {}
+
+
+def _autotune_enabled() -> bool:
+    return os.environ.get("LYNNREAL_AMD_AUTOTUNE", "0") not in ("", "0")
+
+
+def _cache_file(key) -> pathlib.Path:
+    """The tile cache entry of `key` (model/int8_gemm.py:64-66 keeps its own
+    under TRITON_CACHE_DIR; this one lives under LYNNREAL_AMD_CACHE_DIR)."""
+    root = pathlib.Path(os.environ.get("LYNNREAL_AMD_CACHE_DIR",
+                                       pathlib.Path.home() / ".cache" / "lynnreal_amd"))
+    return root / ("int8-" + hashlib.sha256(repr(key).encode()).hexdigest() + ".json")
+
+
+def _prefix(device: torch.device) -> tuple:
+    """What a tuned choice depends on besides the shape: the library's bytes
+    and the device (model/int8_gemm.py:107-113 keys on its sources, Triton,
+    CUDA and the device's name, capability and SM count)."""
+    index = device.index if device.index is not None else torch.cuda.current_device()
+    prefix = _prefixes.get(index)
+    if prefix is None:
+        code = hashlib.sha256(_lib.library_path().read_bytes()).hexdigest()
+        props = torch.cuda.get_device_properties(index)
+        prefix = _prefixes[index] = (code, torch.version.hip, props.name,
+                                     getattr(props, "gcnArchName", ""), props.multi_processor_count)
+    return prefix
+
+
+def _encode(tile):
+    return list(tile) if isinstance(tile, tuple) else tile
+
+
+def _decode(saved):
+    if isinstance(saved, list):
+        saved = tuple(saved)
+    return saved if saved in _CANDIDATES else _MISSING
+
+
+_MISSING = object()
+
+
+def _tuned_tile(a, b, row_scale, column_scale, bias, out, epilogue, residual, table, indices,
+                sequence, gate_slot):
+    """The fastest tile for this call's shape, from memory, from the cache
+    file, or by timing every candidate once the call has run (graph capture
+    takes the library's own choice and records nothing)."""
+    m, k = a.shape
+    n = b.shape[1]
+    key = _prefix(a.device) + (m, n, k, tuple(b.stride()), bias is not None, epilogue)
+    tile = _selected.get(key, _MISSING)
+    if tile is not _MISSING:
+        return tile
+    try:
+        tile = _decode(json.loads(_cache_file(key).read_text()))
+    except (OSError, ValueError, TypeError):
+        tile = _MISSING
+    if tile is not _MISSING:
+        _selected[key] = tile
+        return tile
+    if torch.cuda.is_current_stream_capturing():
+        return None
+    args = (a, b, row_scale, column_scale, bias, out, epilogue)
+    extra = dict(residual=residual, table=table, indices=indices, sequence=sequence,
+                 gate_slot=gate_slot, splits=None)
+    best, best_us = None, float("inf")
+    for candidate in _CANDIDATES:
+        try:
+            _launch(*args, candidate if candidate is not None else "auto", **extra)
+        except ValueError:
+            continue  # a tile this shape does not take
+        times = []
+        for _ in range(3):
+            start = torch.cuda.Event(enable_timing=True)
+            end = torch.cuda.Event(enable_timing=True)
+            start.record()
+            _launch(*args, candidate if candidate is not None else "auto", **extra)
+            end.record()
+            end.synchronize()
+            times.append(start.elapsed_time(end) * 1e3)
+        us = sorted(times)[1]
+        if us < best_us:
+            best, best_us = candidate, us
+    _selected[key] = best
+    try:
+        path = _cache_file(key)
+        path.parent.mkdir(parents=True, exist_ok=True)
+        tmp = path.with_suffix(f".{os.getpid()}.tmp")
+        tmp.write_text(json.dumps(_encode(best)))
+        tmp.replace(path)
+    except OSError:
+        pass  # a read-only cache directory only loses the record
+    return best
 
 
 @functools.lru_cache(maxsize=4096)

@@ -36,6 +36,30 @@ def test_tile_mapping():
             int8_gemm._tile_id(bad)
 
 
+def test_autotune_cache_entries(monkeypatch, tmp_path):
+    """The tile cache (model/int8_gemm.py:64-66,124-151 keeps one JSON file per
+    key): every candidate survives the JSON round trip, anything else reads
+    as absent, the file lives under LYNNREAL_AMD_CACHE_DIR, and autotuning is
+    off unless LYNNREAL_AMD_AUTOTUNE asks for it."""
+    import json
+    for tile in int8_gemm._CANDIDATES:
+        assert int8_gemm._decode(json.loads(json.dumps(int8_gemm._encode(tile)))) == tile
+    for junk in ([32, 32], "fast", 7, {"bm": 256}, [256, 256, 128]):
+        assert int8_gemm._decode(junk) is int8_gemm._MISSING
+    monkeypatch.setenv("LYNNREAL_AMD_CACHE_DIR", str(tmp_path))
+    key = ("lib", "7.2", "gpu", "gfx950", 256, 128, 256, 512, (1, 512), True, 0)
+    path = int8_gemm._cache_file(key)
+    assert path.parent == tmp_path and path.name.startswith("int8-") and path.suffix == ".json"
+    assert int8_gemm._cache_file(key[:-1] + (1,)) != path
+    monkeypatch.delenv("LYNNREAL_AMD_AUTOTUNE", raising=False)
+    assert not int8_gemm._autotune_enabled()
+    monkeypatch.setenv("LYNNREAL_AMD_AUTOTUNE", "0")
+    assert not int8_gemm._autotune_enabled()
+    monkeypatch.setenv("LYNNREAL_AMD_AUTOTUNE", "1")
+    assert int8_gemm._autotune_enabled()
+    assert int8_gemm._tile_id("auto") == int8_gemm._tile_id(None) == _lib.TILE_AUTO
+
+
 def test_tile_ids_match_the_header():
     """Every LR_TILE_* of the C header has the same value in the Python
     bindings, and the named tiles map onto them."""
