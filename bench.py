@@ -7,8 +7,9 @@ replaced by random bf16:
 
   rms_adaln_quant(0,1) -> QKV GEMM (N=15360) -> quantize(attn) ->
   out-proj GEMM (N=5120) + gated residual (slot 2) -> rms_adaln_quant(3,4) ->
-  FFN-up GEMM (N=20480) + GELU-tanh -> quantize -> FFN-down GEMM (K=20480,
-  N=5120) + gated residual (slot 5)
+  FFN-up GEMM (N=20480) -> GELU-tanh + quantize (one row kernel, as the
+  reference fuses its SwiGLU into the re-quantizer) -> FFN-down GEMM
+  (K=20480, N=5120) + gated residual (slot 5)
 
 Inputs are synthetic (the benchmark's own generators: torch.Generator seeded with
 20261201 + config index, N(0,1) activations with 1% outlier channels x20,
@@ -175,9 +176,9 @@ def run_gpu(args, data):
         mark(4)
         q2, s2 = k._rms_adaln_quant_int8(x1, norm2, table, idx, 3, 4)
         mark(5)
-        h = int8_matmul(q2, W["up"][0], s2, W["up"][1], W["up"][2], activation="gelu_tanh")
+        h = int8_matmul(q2, W["up"][0], s2, W["up"][1], W["up"][2])
         mark(6)
-        q3, s3 = k.quantize_rows(h)
+        q3, s3 = k._gelu_quant_int8(h)
         mark(7)
         x2 = int8_matmul(q3, W["down"][0], s3, W["down"][1], W["down"][2], residual=x1, table=table,
                          indices=idx, gate_slot=5)
@@ -494,8 +495,8 @@ def run_splitk(args):
 def run_c4(args):
     """Benchmark config 4: W8A8 FFN at T=65536 against the same shapes in bf16.
 
-    W8A8 step: quantize_rows(x) -> up GEMM (N=20480) + GELU-tanh epilogue ->
-    quantize_rows(h) -> down GEMM (K=20480, N=5120) + bias.
+    W8A8 step: quantize_rows(x) -> up GEMM (N=20480) + bias -> GELU-tanh +
+    quantize (one row kernel) -> down GEMM (K=20480, N=5120) + bias.
     bf16 step: the same weights dequantized to bf16, F.linear (hipBLASLt with
     its bias epilogue) for both projections, F.gelu(approximate="tanh") between,
     as an unquantized Linear -> GELU -> Linear feed-forward runs.
@@ -526,9 +527,9 @@ def run_c4(args):
         ev[0].record()
         q, s = k.quantize_rows(x)
         ev[1].record()
-        h = int8_matmul(q, W["up"][0].t(), s, W["up"][1], W["up"][2], activation="gelu_tanh")
+        h = int8_matmul(q, W["up"][0].t(), s, W["up"][1], W["up"][2])
         ev[2].record()
-        q3, s3 = k.quantize_rows(h)
+        q3, s3 = k._gelu_quant_int8(h)
         ev[3].record()
         y = int8_matmul(q3, W["down"][0].t(), s3, W["down"][1], W["down"][2])
         ev[4].record()
@@ -563,7 +564,7 @@ def run_c4(args):
     ops_up, ops_down = 2 * tokens * hidden * ffn, 2 * tokens * ffn * hidden
     gemm8_us, gemm16_us = t8[1] + t8[3], t16[0] + t16[2]
     step8_us, step16_us = sum(t8), sum(t16)
-    log(json.dumps({"w8a8_us": dict(zip(["quant_x", "up_gelu", "quant_h", "down"], t8)),
+    log(json.dumps({"w8a8_us": dict(zip(["quant_x", "up", "gelu_quant_h", "down"], t8)),
                     "bf16_us": dict(zip(["up_bias", "gelu", "down_bias"], t16)),
                     "cosine_w8a8_vs_bf16": cos}, indent=1))
     return {
@@ -573,12 +574,12 @@ def run_c4(args):
         "ms_per_step": round(step8_us / 1e3, 3), "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "int8", "data": "synthetic (seed 20261201+3), resident in HBM",
         "config": {"workload": "C4 large-shape FFN", "tokens": tokens, "hidden": hidden, "ffn": ffn,
-                   "ffn_activation": "gelu_tanh", "parallelism": "single GPU"},
+                   "ffn_activation": "gelu_tanh (in the re-quantizer)", "parallelism": "single GPU"},
         "gemm_speedup_vs_bf16": round(gemm16_us / gemm8_us, 3),
         "step_speedup_vs_bf16": round(step16_us / step8_us, 3),
         "w8a8": {"up_tops": round(ops_up / (t8[1] * 1e-6) / 1e12, 1),
                  "down_tops": round(ops_down / (t8[3] * 1e-6) / 1e12, 1),
-                 "quant_x_us": round(t8[0], 1), "quant_h_us": round(t8[2], 1),
+                 "quant_x_us": round(t8[0], 1), "gelu_quant_h_us": round(t8[2], 1),
                  "step_us": round(step8_us, 1)},
         "bf16": {"up_tflops": round(ops_up / (t16[0] * 1e-6) / 1e12, 1),
                  "down_tflops": round(ops_down / (t16[2] * 1e-6) / 1e12, 1),
@@ -1180,13 +1181,14 @@ def main():
         "data": "synthetic (N(0,1) activations with 1% outlier channels x20, uniform int8 weights, seed 20261201+2), resident in HBM",
         "config": {"workload": "C3 Flash-block W8A8 projection chain", "tokens": args.tokens,
                    "hidden": args.hidden, "heads": "40x128", "ffn": args.ffn,
-                   "ffn_activation": "gelu_tanh", "gemm_ops_per_step": total_ops,
+                   "ffn_activation": "gelu_tanh (in the re-quantizer)", "gemm_ops_per_step": total_ops,
                    "parallelism": "single GPU"},
         "block_us": round(ms * 1e3, 1),
         "pct_int8_peak": round(100 * total_ops / (ms * 1e-3) / 1e12 / PEAK_INT8_TOPS, 2),
         "gemm_tops": round(total_ops / (gemm_us * 1e-6) / 1e12, 1),
         "kernels": detail,
-        "roofline": {"kernel": "int8 GEMM FFN-up M=12288 K=5120 N=20480 (+GELU epilogue)",
+        "roofline": {"kernel": "int8 GEMM FFN-up M=12288 K=5120 N=20480 (bf16 + bias epilogue; "
+                             "the GELU-tanh runs in the FFN re-quantizer)",
                      "bound": "mfma", "achieved": round(up_tops, 1), "peak": PEAK_INT8_TOPS,
                      "unit": "TOPS", "frac": round(up_tops / PEAK_INT8_TOPS, 4),
                      "traffic": traffic_bytes("up"), "us": round(up_us, 2)},

@@ -229,6 +229,16 @@ int lr_swiglu_quant(const void* p, int8_t* q, float* scales, int64_t rows, int64
  * comfyui/custom_nodes/ComfyUI-LynnReal/tools/verify_sampling_safety.py:59. */
 int lr_gelu_tanh(const void* x, void* out, int64_t count, void* stream);
 
+/* GELU-tanh fused with the per-row INT8 quantizer, the FFN re-quantization of
+ * a GELU-tanh FFN: a = bf16(gelu_tanh(x)) as lr_gelu_tanh computes it, then
+ * q/scales as lr_quantize_rows. The GELU counterpart of lr_swiglu_quant
+ * (model/kernels.py:318-328, which fuses the reference's FFN activation into
+ * its re-quantizer); equal bit for bit to lr_gelu_tanh followed by
+ * lr_quantize_rows. x bf16 [rows, width]; q int8 [rows, width]; scales fp32
+ * [rows]. */
+int lr_gelu_quant(const void* x, int8_t* q, float* scales, int64_t rows, int64_t width,
+                  void* stream);
+
 /* Per-head RMSNorm of Q and K fused with rotary embedding. Replaces the
  * launches at model/fusion.py:35-52 of model/kernels.py:187-257
  * (_qk_norm_full_rope_paired_kernel, rotary_dim == head_dim) and :345-402

@@ -55,6 +55,7 @@ SIGNATURES = {
     "lr_swiglu": [_P, _P, _I64, _I64, _P],
     "lr_swiglu_quant": [_P, _P, _P, _I64, _I64, _P],
     "lr_gelu_tanh": [_P, _P, _I64, _P],
+    "lr_gelu_quant": [_P, _P, _P, _I64, _I64, _P],
     "lr_qk_norm_rope": [_P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64,
                         _I64, _I64, _F32, _P],
     "lr_gather_rows": [_P, _P, _P, _I64, _I64, _I64, _I64, _P],

@@ -175,6 +175,79 @@ __global__ __launch_bounds__(kThreads) void gelu_any(const uint16_t* __restrict_
   out[e] = (uint16_t)(pack_bf2(fast_gelu_tanh(bf_to_f(x[e])), 0.0f) & 0xffffu);
 }
 
+// GELU-tanh + per-row INT8 quantizer in one pass over the FFN-up output:
+// the GELU counterpart of swiglu_quant (the reference fuses its FFN
+// activation into the re-quantizer the same way, model/kernels.py:169-185).
+// Each value becomes bf16(gelu_tanh(x)) with fast_gelu_tanh, as the GEMM's
+// GELU epilogue computes it, so gelu_quant(y) equals quantize_rows of that
+// epilogue's output bit for bit. One block per row, the activated row in
+// fp32 registers between the absmax and the quotient.
+template <int CPT>
+__global__ __launch_bounds__(kThreads) void gelu_quant_vec(const uint4* __restrict__ x,
+                                                           uint2* __restrict__ q,
+                                                           float* __restrict__ scales,
+                                                           int64_t chunks) {
+  __shared__ float red[4];
+  const int64_t row = blockIdx.x;
+  const uint4* src = x + row * chunks;
+  uint2* dst = q + row * chunks;
+  uint4 v[CPT];
+#pragma unroll
+  for (int i = 0; i < CPT; ++i) {
+    const int64_t c = threadIdx.x + i * kThreads;
+    v[i] = c < chunks ? load_nt(src + c) : make_uint4(0, 0, 0, 0);
+  }
+  float a[CPT][8];
+  float m = 0.0f;
+#pragma unroll
+  for (int i = 0; i < CPT; ++i) {
+    unpack8(v[i], a[i]);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      a[i][e] = round_bf(fast_gelu_tanh(a[i][e]));  // gelu(0) = 0 past the row end
+      m = fmaxf(m, __builtin_fabsf(a[i][e]));
+    }
+  }
+  m = block256_max(m, red);
+  const float s = quant_scale(m);
+  const float inv = 1.0f / s;
+  if (m < 0x1p80f) {  // the three-operation quotient (quantize.hip, norm.hip)
+    const float lo = quant_lo(s, inv);
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+      const int64_t c = threadIdx.x + i * kThreads;
+      if (c < chunks) dst[c] = quant8_split(a[i], inv, lo);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < CPT; ++i) {
+      const int64_t c = threadIdx.x + i * kThreads;
+      if (c < chunks) dst[c] = quant8(a[i], s, inv);
+    }
+  }
+  if (threadIdx.x == 0) scales[row] = s;
+}
+
+// Any width or alignment: the activation is recomputed in the second pass
+// (same arithmetic, so the same values).
+__global__ __launch_bounds__(kThreads) void gelu_quant_any(const uint16_t* __restrict__ x,
+                                                           int8_t* __restrict__ q,
+                                                           float* __restrict__ scales,
+                                                           int64_t width) {
+  __shared__ float red[4];
+  const int64_t row = blockIdx.x;
+  const uint16_t* src = x + row * width;
+  float m = 0.0f;
+  for (int64_t c = threadIdx.x; c < width; c += kThreads)
+    m = fmaxf(m, __builtin_fabsf(round_bf(fast_gelu_tanh(bf_to_f(src[c])))));
+  m = block256_max(m, red);
+  const float s = quant_scale(m);
+  const float inv = 1.0f / s;
+  for (int64_t c = threadIdx.x; c < width; c += kThreads)
+    q[row * width + c] = (int8_t)quant_one(round_bf(fast_gelu_tanh(bf_to_f(src[c]))), s, inv);
+  if (threadIdx.x == 0) scales[row] = s;
+}
+
 int blocks_for(int64_t work, unsigned* out) {
   const int64_t b = (work + kThreads - 1) / kThreads;
   if (b > 0x7fffffffLL) return fail(LR_EUNSUPPORTED, "elementwise: problem too large (not supported)");
@@ -268,4 +341,31 @@ extern "C" int lr_gelu_tanh(const void* x, void* out, int64_t count, void* strea
     hipLaunchKernelGGL(gelu_any, dim3(blocks), dim3(kThreads), 0, st, (const uint16_t*)x,
                        (uint16_t*)out, count);
   return check_launch("gelu_tanh");
+}
+
+extern "C" int lr_gelu_quant(const void* x, int8_t* q, float* scales, int64_t rows, int64_t width,
+                             void* stream) {
+  LR_REQUIRE(rows >= 0 && width > 0, "gelu_quant: bad shape");
+  if (rows == 0) return LR_OK;
+  LR_REQUIRE(x && q && scales, "gelu_quant: null pointer");
+  LR_REQUIRE(rows <= 0x7fffffffLL, "gelu_quant: too many rows");
+  hipStream_t st = as_stream(stream);
+  const int64_t chunks = width / 8;
+  const bool vec = width % 8 == 0 && aligned(x, 16) && aligned(q, 8) && chunks <= 16 * kThreads;
+  const dim3 grid((unsigned)rows), block(kThreads);
+  if (vec) {
+    const int64_t need = (chunks + kThreads - 1) / kThreads;
+    const uint4* src = static_cast<const uint4*>(x);
+    uint2* dst = reinterpret_cast<uint2*>(q);
+    if (need <= 1) hipLaunchKernelGGL(gelu_quant_vec<1>, grid, block, 0, st, src, dst, scales, chunks);
+    else if (need <= 2) hipLaunchKernelGGL(gelu_quant_vec<2>, grid, block, 0, st, src, dst, scales, chunks);
+    else if (need <= 4) hipLaunchKernelGGL(gelu_quant_vec<4>, grid, block, 0, st, src, dst, scales, chunks);
+    else if (need <= 8) hipLaunchKernelGGL(gelu_quant_vec<8>, grid, block, 0, st, src, dst, scales, chunks);
+    else if (need <= 10) hipLaunchKernelGGL(gelu_quant_vec<10>, grid, block, 0, st, src, dst, scales, chunks);
+    else hipLaunchKernelGGL(gelu_quant_vec<16>, grid, block, 0, st, src, dst, scales, chunks);
+  } else {
+    hipLaunchKernelGGL(gelu_quant_any, grid, block, 0, st, static_cast<const uint16_t*>(x), q, scales,
+                       width);
+  }
+  return check_launch("gelu_quant");
 }

@@ -17,6 +17,7 @@ Arithmetic (all fp32 with the reference's bf16 rounding points):
   _gated_residual      bf16(x + bf16(gate*u))                 kernels.py:131-153
   _swiglu(_quant)      bf16(v * bf16(g*sigmoid(g))) (-> INT8)  kernels.py:156-185
   gelu_tanh            bf16(gelu_tanh(x))  (new: the benchmark FFN activation)
+  _gelu_quant_int8     quantize_rows(gelu_tanh(x)) in one pass (new)
   qk_norm_rope         per-head RMSNorm of Q/K -> bf16, RoPE with bf16 products
                                                               kernels.py:187-257,345-402
   adaln_table          bf16(bf16(silu(temb)) @ W^T + bias)     fusion.py:68-69
@@ -220,6 +221,22 @@ def gelu_tanh(value):
     _lib.call("lr_gelu_tanh", value.data_ptr(), output.data_ptr(), value.numel(),
               _lib.stream(value))
     return output
+
+
+def _gelu_quant_int8(value):
+    """GELU-tanh + INT8 quant of [.., width] rows -> (int8 [rows, width],
+    fp32 [rows, 1]): quantize_rows(gelu_tanh(value)) in one pass, the GELU
+    counterpart of _swiglu_quant_int8 (model/kernels.py:318-328)."""
+    value = _bf16(value, "value")
+    _lib.check_device(value)
+    width = value.shape[-1]
+    rows = value.numel() // width if width else 0
+    value = value.reshape(rows, width).contiguous()
+    output = torch.empty((rows, width), device=value.device, dtype=torch.int8)
+    scales = torch.empty((rows, 1), device=value.device, dtype=torch.float32)
+    _lib.call("lr_gelu_quant", value.data_ptr(), output.data_ptr(), scales.data_ptr(), rows, width,
+              _lib.stream(value))
+    return output, scales
 
 
 def qk_norm_rope(query, key, query_weight, key_weight, rotary_emb, eps):

@@ -94,4 +94,10 @@ def gelu_tanh(x):
     return _done(kernels.gelu_tanh(_t(x)))
 
 
+def gelu_quant(x):
+    q, s = kernels._gelu_quant_int8(_t(x))
+    q, s = _done(q, s)
+    return q, s.reshape(-1)
+
+
 module = types.SimpleNamespace(**{k: v for k, v in globals().items() if callable(v) and not k.startswith("_")})
