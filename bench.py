@@ -408,6 +408,10 @@ def run_c5(args):
                         "tops": round(2 * 256 * n * kk / (us * 1e-6) / 1e12, 1)}
         if n == 5120 and kk == 5120:
             skinny[name]["eager"] = _eager_calls(lambda: int8_matmul(a, w.t(), rs, cs))
+        # hipBLASLt's INT8 GEMM on the same operands (int32 out, no epilogue): a
+        # yardstick for these weight-streaming shapes.
+        wt = w.t()
+        skinny[name]["hipblaslt_int_mm_us"] = round(_event_time(lambda: torch._int_mm(a, wt), 50), 2)
     return {"metric": "C5 ragged chain TOPS (T=12605, per-frame modulation) + M=256 projections",
             "value": round(sum(ops.values()) / (ms * 1e-3) / 1e12, 2), "unit": "TOPS", "n_gpus": 1,
             "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4),
