@@ -115,14 +115,31 @@ def raise_for(status: int, name: str) -> None:
     raise RuntimeError(message)
 
 
+try:
+    from . import _pycall
+except ImportError:  # not built: every call goes through ctypes
+    _pycall = None
+
 _entry: dict[str, object] = {}
+
+
+def _bind(name: str):
+    """The callable for entry point `name`: the _pycall fast call with the
+    function's address when every argument is a pointer or an integer, else
+    the ctypes function (entry points with float arguments)."""
+    fn = getattr(load(), name)
+    if _pycall is not None and all(t in (_P, _I64, _I32) for t in SIGNATURES[name]):
+        address = ctypes.cast(fn, ctypes.c_void_p).value
+        fast = _pycall.call
+        return lambda *args: fast(address, *args)
+    return fn
 
 
 def call(name: str, *args) -> None:
     """Call entry point `name` and raise on a non-zero status."""
     fn = _entry.get(name)
     if fn is None:
-        fn = _entry[name] = getattr(load(), name)
+        fn = _entry[name] = _bind(name)
     status = fn(*args)
     if status:
         raise_for(status, name)
@@ -149,8 +166,9 @@ def same_device(primary: torch.Tensor, **tensors) -> None:
     `primary`'s device. The kernels receive raw pointers, so a host tensor or
     one on another GPU must be refused here, before any launch."""
     index = primary.get_device()
-    for name, t in tensors.items():
+    for t in tensors.values():
         if t is not None and t.get_device() != index:
+            name = next(k for k, v in tensors.items() if v is t)
             raise ValueError(f"{name} is on {t.device}, but the kernel runs on {primary.device}")
 
 

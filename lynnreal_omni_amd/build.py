@@ -3,7 +3,8 @@
 Usage: python -m lynnreal_omni_amd.build  (or build() from Python).
 
 Every .hip file under csrc/ is compiled for gfx950 only, in parallel, and
-linked into lynnreal_omni_amd/liblynnreal_amd.so. The library is written to
+linked into lynnreal_omni_amd/liblynnreal_amd.so; csrc/pycall.c becomes the
+CPython module _pycall beside it. The library is written to
 a temporary name and renamed into place, so a process that has the old one
 loaded keeps a valid mapping.
 """
@@ -14,6 +15,7 @@ import os
 import pathlib
 import shutil
 import subprocess
+import sysconfig
 
 HERE = pathlib.Path(__file__).resolve().parent
 ROOT = HERE.parent
@@ -60,8 +62,28 @@ def _compile(src: pathlib.Path, extra: list[str]) -> pathlib.Path:
     return obj
 
 
+PYCALL = HERE / ("_pycall" + (sysconfig.get_config_var("EXT_SUFFIX") or ".so"))
+
+
+def build_pycall() -> pathlib.Path:
+    """Compile csrc/pycall.c, the CPython fast-call shim of the integer-argument
+    entry points, with the host C compiler (no GPU code in it)."""
+    cc = shutil.which("gcc") or shutil.which("cc")
+    if cc is None:
+        raise RuntimeError("no C compiler found for csrc/pycall.c")
+    tmp = PYCALL.with_name(PYCALL.name + f".tmp{os.getpid()}")
+    cmd = [cc, "-O2", "-shared", "-fPIC", "-Wall", f"-I{sysconfig.get_paths()['include']}",
+           str(CSRC / "pycall.c"), "-o", str(tmp)]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"pycall.c failed:\n{proc.stderr}")
+    os.replace(tmp, PYCALL)
+    return PYCALL
+
+
 def build(extra: list[str] | None = None, jobs: int = 8) -> pathlib.Path:
-    """Compile every csrc/*.hip for gfx950 and link the shared library."""
+    """Compile every csrc/*.hip for gfx950 and link the shared library (and
+    the CPython fast-call shim beside it)."""
     extra = list(extra or [])
     OBJ.mkdir(exist_ok=True)
     sources = sorted(CSRC.glob("*.hip"))
@@ -75,6 +97,7 @@ def build(extra: list[str] | None = None, jobs: int = 8) -> pathlib.Path:
     if proc.returncode != 0:
         raise RuntimeError(f"link failed:\n{proc.stderr}")
     os.replace(tmp, LIBRARY)
+    build_pycall()
     return LIBRARY
 
 

@@ -9,7 +9,7 @@ Differences from the reference, by design:
   * No Triton. The kernel's tile is chosen by shape inside the library;
     `tile=` accepts the reference's tile tuples (BM, BN, BK, warps, stages[,
     group]) and maps (BM, BN) onto the HIP tile of the same shape, or raises
-    ValueError. With LYNNREAL_AMD_AUTOTUNE=1 the first call of each shape
+    ValueError. With LYNNREAL_AMD_AUTOTUNE=1 (read at import) the first call of each shape
     times every HIP tile instead and keeps the fastest in memory and in a JSON
     file keyed by library, device and shape (the reference's autotuner and
     tile cache, model/int8_gemm.py:53-81,124-151); every tile computes the
@@ -82,16 +82,22 @@ def _launch(a, b, row_scale, column_scale, bias, out, epilogue, tile, residual=N
     if table is not None:
         table_width = table.shape[-1]
         table_rows = table.numel() // table_width
-    if tile is None and splits is None and _autotune_enabled():
+    if tile is None and splits is None and _AUTOTUNE:
         tile = _tuned_tile(a, b, row_scale, column_scale, bias, out, epilogue, residual, table,
                            indices, sequence, gate_slot)
-    tile_id = _tile_id(tile)
+    tile_id = _lib.TILE_AUTO if tile is None else _tile_id(tile)
     splits = 0 if splits is None else int(splits)
-    ws, ws_bytes = _lib.workspace(a, _workspace_bytes(m, n, k, splits, tile_id))
-    _lib.call("lr_int8_gemm_ws", a.data_ptr(), b.data_ptr(), b.stride(0), b.stride(1), m, n, k,
-              _lib.ptr(row_scale), _lib.ptr(column_scale), _lib.ptr(bias), out.data_ptr(),
-              epilogue, _lib.ptr(residual), _lib.ptr(table), table_rows, table_width,
-              _lib.ptr(indices), sequence, gate_slot, ws, ws_bytes, splits, tile_id, _lib.stream(a))
+    nbytes = _workspace_bytes(m, n, k, splits, tile_id)
+    ws, ws_bytes = _lib.workspace(a, nbytes) if nbytes else (None, 0)
+    sb0, sb1 = b.stride()
+    _lib.call("lr_int8_gemm_ws", a.data_ptr(), b.data_ptr(), sb0, sb1, m, n, k,
+              None if row_scale is None else row_scale.data_ptr(),
+              None if column_scale is None else column_scale.data_ptr(),
+              None if bias is None else bias.data_ptr(), out.data_ptr(), epilogue,
+              None if residual is None else residual.data_ptr(),
+              None if table is None else table.data_ptr(), table_rows, table_width,
+              None if indices is None else indices.data_ptr(), sequence, gate_slot, ws, ws_bytes,
+              splits, tile_id, _lib.stream(a))
     return out
 
 
@@ -105,7 +111,13 @@ _prefixes: dict[int, tuple] = {}
 
 
 def _autotune_enabled() -> bool:
+    """LYNNREAL_AMD_AUTOTUNE as a flag ("", "0" or unset: off)."""
     return os.environ.get("LYNNREAL_AMD_AUTOTUNE", "0") not in ("", "0")
+
+
+# Read once at import, as the reference reads its LYNNREAL_* switches
+# (model/int8_gemm.py:57): an environment lookup costs half a microsecond per call.
+_AUTOTUNE = _autotune_enabled()
 
 
 def _cache_file(key) -> pathlib.Path:
@@ -223,8 +235,11 @@ def int8_matmul(a, b, row_scale, column_scale, bias=None, *, tile=None, activati
     if a.dtype != torch.int8 or b.dtype != torch.int8 or not a.is_contiguous() or a.shape[1] != b.shape[0]:
         raise ValueError("INT8 GEMM requires contiguous row-major activations and compatible INT8 weights")
     _lib.check_device(a)
-    _lib.same_device(a, b=b, row_scale=row_scale, column_scale=column_scale, bias=bias,
-                     residual=residual, table=table, indices=indices)
+    if residual is None:
+        _lib.same_device(a, b=b, row_scale=row_scale, column_scale=column_scale, bias=bias)
+    else:
+        _lib.same_device(a, b=b, row_scale=row_scale, column_scale=column_scale, bias=bias,
+                         residual=residual, table=table, indices=indices)
     m, k = a.shape
     n = b.shape[1]
     row_scale = _f32_vector(row_scale)

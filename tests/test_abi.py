@@ -123,3 +123,72 @@ def test_split_k_workspace_sizes_and_checks_without_a_gpu(lib):
     rc = lib.lr_int8_gemm_ws(p, p, 1, 1024, 64, 128, 1024, p, p, None, p, 0, None, None, 0, 0, None, 0, 0,
                              None, 0, 65, _lib.TILE_AUTO, None)
     assert rc == _lib.LR_EINVAL and b"splits" in lib.lr_last_error()
+
+
+def test_fast_call_shim_is_built_and_bound():
+    """build() puts the CPython fast-call module beside the library; the
+    integer-argument entry points go through it and the ones with float
+    arguments (eps) stay on ctypes."""
+    from lynnreal_omni_amd import _pycall  # noqa: F401  (fails loudly if not built)
+    assert _lib._pycall is not None
+    fast = _lib._bind("lr_int8_gemm_ws")
+    slow = _lib._bind("lr_rms_adaln")
+    assert not isinstance(fast, ctypes._CFuncPtr) and isinstance(slow, ctypes._CFuncPtr)
+
+
+def test_fast_call_matches_ctypes_statuses(lib):
+    """The same invalid calls give the same statuses and messages through the
+    shim as through ctypes (validation runs before any GPU call)."""
+    cases = [
+        ("lr_quantize_rows", (None, -1, 8, None, None, None), b"negative shape"),
+        ("lr_quantize_rows", (None, 1, 8, None, None, None), b"null"),
+        ("lr_int8_gemm", (None, None, 1, 1, 4, 4, 4, None, None, None, None, 99, None, None, 0, 0,
+                          None, 0, 0, 0, None), b"epilogue"),
+        ("lr_int8_gemm_ws", (None, None, 1, 1, 4, 4, 4, None, None, None, None, 0, None, None, 0, 0,
+                             None, 0, 0, None, 0, 0, 99, None), b"unknown tile"),
+        ("lr_int8_gemm_ws", (None, None, 1, 1, 4, 4, 4, None, None, None, None, 0, None, None, 0, 0,
+                             None, 0, 0, None, -5, 0, 0, None), b"workspace"),
+        ("lr_gelu_quant", (None, None, None, 3, 0, None), b"bad shape"),
+    ]
+    for name, args, message in cases:
+        fast = _lib._bind(name)(*args)
+        fast_msg = lib.lr_last_error()
+        slow = getattr(lib, name)(*args)
+        assert fast == slow == _lib.LR_EINVAL and message in fast_msg and fast_msg == lib.lr_last_error()
+    assert _lib._bind("lr_quantize_rows")(None, 0, 8, None, None, None) == _lib.LR_OK
+
+
+def test_fast_call_passes_every_argument(tmp_path):
+    """All 24 argument slots of the shim, mixing int and int64_t parameters as
+    the GEMM entry point does, with negative values, None (0) and large
+    pointer-like values, reach a C function intact (a helper compiled here)."""
+    import shutil
+    from lynnreal_omni_amd import _pycall
+    cc = shutil.which("gcc") or shutil.which("cc")
+    if cc is None:
+        pytest.skip("no C compiler")
+    src = tmp_path / "probe.c"
+    params = ", ".join(f"{'int' if i % 3 == 1 else 'long long'} a{i}" for i in range(24))
+    body = " ".join(f"h = h * 1000003ULL ^ (unsigned long long)(long long)a{i};" for i in range(24))
+    src.write_text("static unsigned long long h;\n"
+                   f"int probe({params}) {{ h = 0; {body} return (int)(h ^ (h >> 32)); }}\n")
+    so = tmp_path / "libprobe.so"
+    subprocess.run([cc, "-O1", "-shared", "-fPIC", str(src), "-o", str(so)], check=True)
+    fn = ctypes.CDLL(str(so)).probe
+    address = ctypes.cast(fn, ctypes.c_void_p).value
+    values = [(-1) ** i * (i * 7919 + 3) for i in range(24)]
+    values[2], values[5], values[8] = None, 0x7fff_dead_beef_0000, -(2 ** 40)
+    values[10] = 2 ** 31 - 1   # an int parameter at its maximum
+    expect_h = 0
+    for i, v in enumerate(values):
+        x = 0 if v is None else v
+        if i % 3 == 1:
+            x = ((x + 2 ** 31) % 2 ** 32) - 2 ** 31   # what an int parameter reads
+        expect_h = ((expect_h * 1000003) % 2 ** 64) ^ (x % 2 ** 64)
+    folded = (expect_h ^ (expect_h >> 32)) % 2 ** 32
+    expect = folded - 2 ** 32 if folded >= 2 ** 31 else folded
+    assert _pycall.call(address, *values) == expect
+    with pytest.raises(TypeError):
+        _pycall.call(address, 1.5)
+    with pytest.raises(TypeError):
+        _pycall.call(address, *range(25))

@@ -19,7 +19,8 @@ pytestmark = pytest.mark.gpu
 
 @pytest.fixture
 def tuning(monkeypatch, tmp_path):
-    monkeypatch.setenv("LYNNREAL_AMD_AUTOTUNE", "1")
+    # The switch is read at import (LYNNREAL_AMD_AUTOTUNE=1); set it as that would.
+    monkeypatch.setattr(int8_gemm, "_AUTOTUNE", True)
     monkeypatch.setenv("LYNNREAL_AMD_CACHE_DIR", str(tmp_path))
     int8_gemm._selected.clear()
     yield tmp_path
