@@ -5,7 +5,9 @@
  * launch Triton kernels; it has no FFI. Each entry point below replaces one
  * of those functions and cites it (paths relative to the reference checkout).
  * The Python host layer in lynnreal_omni_amd/ keeps the reference's Python
- * signatures and calls these entry points through ctypes.
+ * signatures and calls these entry points through ctypes (the integer-argument
+ * ones through a CPython fast-call shim); tests/abi_host/c_abi_consumer.cpp is
+ * a C++ host that uses them directly.
  *
  * Conventions shared by every entry point:
  *   - All tensor arguments are raw device pointers. bf16 tensors are passed as

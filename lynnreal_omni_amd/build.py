@@ -81,6 +81,30 @@ def build_pycall() -> pathlib.Path:
     return PYCALL
 
 
+ABI_CONSUMER = ROOT / "tests" / "abi_host" / "c_abi_consumer"
+
+
+def build_abi_consumer() -> pathlib.Path:
+    """Compile tests/abi_host/c_abi_consumer.cpp, a C++ host program that uses
+    the library through include/lynnreal_amd.h alone (host code, no GPU code),
+    against the library built here; a GPU test runs it."""
+    cxx = shutil.which("g++") or shutil.which("c++")
+    src = ABI_CONSUMER.with_suffix(".cpp")
+    if cxx is None or not src.exists():
+        raise RuntimeError("no C++ compiler or no tests/abi_host/c_abi_consumer.cpp")
+    rocm = pathlib.Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
+    tmp = ABI_CONSUMER.with_name(ABI_CONSUMER.name + f".tmp{os.getpid()}")
+    cmd = [cxx, "-O2", "-std=c++17", "-ffp-contract=off", "-Wall", "-D__HIP_PLATFORM_AMD__",
+           f"-I{rocm / 'include'}", f"-I{ROOT / 'include'}", str(src), "-o", str(tmp),
+           f"-L{HERE}", "-llynnreal_amd", f"-L{rocm / 'lib'}", "-lamdhip64",
+           "-Wl,-rpath,$ORIGIN/../../lynnreal_omni_amd", f"-Wl,-rpath,{rocm / 'lib'}"]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"c_abi_consumer.cpp failed:\n{proc.stderr}")
+    os.replace(tmp, ABI_CONSUMER)
+    return ABI_CONSUMER
+
+
 def build(extra: list[str] | None = None, jobs: int = 8) -> pathlib.Path:
     """Compile every csrc/*.hip for gfx950 and link the shared library (and
     the CPython fast-call shim beside it)."""
@@ -98,6 +122,7 @@ def build(extra: list[str] | None = None, jobs: int = 8) -> pathlib.Path:
         raise RuntimeError(f"link failed:\n{proc.stderr}")
     os.replace(tmp, LIBRARY)
     build_pycall()
+    build_abi_consumer()
     return LIBRARY
 
 
