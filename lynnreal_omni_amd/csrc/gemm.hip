@@ -884,6 +884,9 @@ __device__ __forceinline__ void store_tile_passes(const GemmArgs& p, const v4i (
     csv[j] = *reinterpret_cast<const float4*>(p.cs + c);
     if (BIAS) bv[j] = *reinterpret_cast<const uint2*>(p.bias + c);
   }
+  // Everything issued before these loads, the next tile's first operand DMAs
+  // among them, has landed once they have (gemm_stream's k-loop relies on it).
+  __builtin_amdgcn_s_waitcnt(0x70 | 0xf00);  // vmcnt(0)
   const bool seq_covers = p.sequence >= p.m;
   // Unrolled: the accumulator indices must be constants, or the array would
   // live in scratch memory.
@@ -962,7 +965,7 @@ __device__ __forceinline__ void store_tile_passes(const GemmArgs& p, const v4i (
   }
 }
 
-template <int EPI, bool BIAS>
+template <int EPI, bool BIAS, bool STAGED>
 __global__ __launch_bounds__(512) void gemm_stream(GemmArgs p) {
   constexpr int BM = 256, BN = 256, BK = 128, NA = 3, NB = 2, WAVES_N = 4;
   constexpr int WM = 128, WN = 64, FM = 8, FN = 4;
@@ -1017,6 +1020,21 @@ __global__ __launch_bounds__(512) void gemm_stream(GemmArgs p) {
   constexpr int kWaitA = 0x70 | 0xf00 | PA;  // vmcnt(PA): all but the newest k-step landed
   constexpr int kWaitB = 0x70 | 0xf00 | PB;
   constexpr int kWaitLds = 0xc07f;           // lgkmcnt(0)
+  // With the staged epilogue, k-step 1 of every tile has landed before its
+  // k-loop starts: the first tile's prologue waits for both of its k-steps,
+  // and each epilogue waits for its scale loads, issued after the DMAs of the
+  // next tile's k-steps 0 and 1 (vmcnt counts in issue order). The loop then
+  // skips the wait after k-step 0, the only one that the previous tile's
+  // output stores (issued after those DMAs) would otherwise hold up: they
+  // drain under the MFMAs of k-steps 0 and 1, and the wait for k-step 2,
+  // whose DMAs were issued after them, is the first to cover them.
+  constexpr int kWaitAll = 0x70 | 0xf00;  // vmcnt(0)
+  static_assert(PA == 8 && PB == 8, "wait_after_first_kstep waits for vmcnt(8)");
+  // vmcnt(8) except after k-step 0, as one asm statement: a branch in C++
+  // made the compiler peel k-step 0 out of the loop and spill registers.
+  auto wait_after_first_kstep = [](int kt) {
+    asm volatile("s_cmp_eq_u32 %0, 0\n\ts_cbranch_scc1 1f\n\ts_waitcnt vmcnt(8)\n1:" ::"s"(kt) : "scc");
+  };
 
   int g = 0;  // the workgroup's k-steps before this tile (ring position)
   for (int pid = blockIdx.x; pid < tiles; pid += gridDim.x, g += KT) {
@@ -1078,13 +1096,13 @@ __global__ __launch_bounds__(512) void gemm_stream(GemmArgs p) {
     };
     // The schedule of gemm_fast's ping-pong loop. A later tile's k-steps 0
     // and 1 were issued by the tile before it, whose last waits (A(KT) and
-    // W(KT)) covered k-step 0; the first waits in the loop (all but the newest
-    // k-step landed) then also wait for the previous tile's output stores.
+    // W(KT)) covered k-step 0; the first waits in the loop (k-step 1 landed)
+    // skip the previous tile's output stores where their count is known.
     if (grp == 0) {
       if (first) {
         pdma_a(0);
         pdma_a(1);
-        __builtin_amdgcn_s_waitcnt(kWaitA);
+        __builtin_amdgcn_s_waitcnt(STAGED ? kWaitAll : kWaitA);
       }
       barrier();
       for (int kt = 0; kt < KT; ++kt) {
@@ -1094,7 +1112,10 @@ __global__ __launch_bounds__(512) void gemm_stream(GemmArgs p) {
         barrier();
         compute();  // phase 2kt + 1
         __builtin_amdgcn_sched_barrier(0);
-        __builtin_amdgcn_s_waitcnt(kWaitA);
+        if (STAGED)
+          wait_after_first_kstep(kt);
+        else
+          __builtin_amdgcn_s_waitcnt(kWaitA);
         barrier();
       }
       barrier();  // phase 2KT: group 1 computes the last k-step
@@ -1102,7 +1123,7 @@ __global__ __launch_bounds__(512) void gemm_stream(GemmArgs p) {
       if (first) {
         pdma_b(0);
         pdma_b(1);
-        __builtin_amdgcn_s_waitcnt(kWaitB);
+        __builtin_amdgcn_s_waitcnt(STAGED ? kWaitAll : kWaitB);
       }
       barrier();
       barrier();  // phase 0: group 0 reads k-step 0
@@ -1112,7 +1133,10 @@ __global__ __launch_bounds__(512) void gemm_stream(GemmArgs p) {
         // rows it refills.
         __builtin_amdgcn_s_waitcnt(kWaitLds);
         pdma_b(kt + 2);
-        __builtin_amdgcn_s_waitcnt(kWaitB);  // W(kt + 1) landed
+        if (STAGED)  // W(kt + 1) landed
+          wait_after_first_kstep(kt);
+        else
+          __builtin_amdgcn_s_waitcnt(kWaitB);
         barrier();
         compute();  // phase 2kt + 2
         barrier();
@@ -1122,11 +1146,16 @@ __global__ __launch_bounds__(512) void gemm_stream(GemmArgs p) {
     // epilogue; the slots of the next tile's k-steps 0 and 1 stay untouched.
     // The next tile's first barrier keeps its A(2) DMA, which refills this
     // slot, behind every wave's epilogue.
-    char* const stage = a_ring + ((g + KT - 1) % NA) * A_BYTES + wave * 4096;
-    if (EPI != EPI_RAW && p.staged)
+    // One epilogue per instantiation: a loop whose body held both would merge
+    // their pending loads at the loop head, and the compiler would then wait
+    // for every outstanding memory operation (vmcnt(0)), the output stores
+    // included, before the next tile's accumulators are cleared.
+    if constexpr (STAGED) {
+      char* const stage = a_ring + ((g + KT - 1) % NA) * A_BYTES + wave * 4096;
       store_tile_passes<EPI, BIAS>(p, acc, stage, m0, n0, wm, wn, lane);
-    else
+    } else {
       store_tile<FM, FN, WM, WN, EPI, BIAS>(p, acc, m0, n0, wm, wn, lane);
+    }
   }
   // The last tile's trailing DMAs land before the workgroup's LDS is freed.
   __builtin_amdgcn_s_waitcnt(0x70 | 0xf00);  // vmcnt(0)
@@ -1260,8 +1289,14 @@ void launch_persistent(GemmArgs& p, hipStream_t st) {
   p.tiles_n = (int)((p.n + 255) / 256);
   const int64_t tiles = (int64_t)p.tiles_m * p.tiles_n;
   const int64_t cus = compute_units() >= 8 ? compute_units() / 8 * 8 : 8;
-  hipLaunchKernelGGL((gemm_stream<EPI, BIAS>), dim3((unsigned)(tiles < cus ? tiles : cus)), dim3(512), 0, st,
-                     p);
+  const dim3 grid((unsigned)(tiles < cus ? tiles : cus));
+  if constexpr (EPI != EPI_RAW) {
+    if (p.staged) {
+      hipLaunchKernelGGL((gemm_stream<EPI, BIAS, true>), grid, dim3(512), 0, st, p);
+      return;
+    }
+  }
+  hipLaunchKernelGGL((gemm_stream<EPI, BIAS, false>), grid, dim3(512), 0, st, p);
 }
 
 template <int EPI, bool BIAS>

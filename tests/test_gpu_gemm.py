@@ -294,12 +294,15 @@ def test_c4_shapes_beyond_2gib():
     assert np.array_equal(acc[rows_d].cpu().numpy(), ref.int_mm(want_q, w_dn.cpu().numpy()))
 
 
-@pytest.mark.parametrize("m,n,k", [(1024, 768, 1024), (16385, 5376, 7168), (20000, 2560, 384)])
+@pytest.mark.parametrize("m,n,k", [(1024, 768, 1024), (16385, 5376, 7168), (20000, 2560, 384),
+                                   (8200, 2056, 256)])
 def test_int8_tma_entry_matches_int8_matmul(m, n, k):
     """model/int8_tma.py:33-41's entry point (the persistent GEMM): same output
     as int8_matmul, and the reference's tile tuples map onto HIP tiles. The
     long-M shapes (the reference's M >= 16384 regime) give each of the 256
-    workgroups 3-6 tiles, with M and N tails."""
+    workgroups 3-6 tiles, with M and N tails; 8200 x 2056 x 256 gives some
+    workgroups a second tile two k-steps long (the shortest streamed loop),
+    after a full tile or an edge tile, and checks the GELU epilogue too."""
     from lynnreal_omni_amd import int8_tma
     g = gen(16 + m)
     a = torch.randint(-127, 128, (m, k), dtype=torch.int8, generator=g).cuda()
@@ -314,6 +317,10 @@ def test_int8_tma_entry_matches_int8_matmul(m, n, k):
     want = ref.dequant(ref.int_mm(a[rows].cpu().numpy(), w.cpu().numpy()), rs[rows].cpu().numpy(),
                        cs.cpu().numpy(), to_np(bias))
     assert np.array_equal(to_np(y[rows]), want)
+    if k == 256:
+        gelu = int8_gemm.int8_matmul(a, w.t(), rs, cs, bias, tile="persistent", activation="gelu_tanh")
+        assert torch.equal(gelu, int8_gemm.int8_matmul(a, w.t(), rs, cs, bias, tile=(128, 128),
+                                                       activation="gelu_tanh"))
 
 
 @pytest.mark.parametrize("act", [None, "gelu_tanh", "swiglu"])
