@@ -27,6 +27,7 @@ import hashlib
 import json
 import os
 import pathlib
+import threading
 
 import torch
 
@@ -200,7 +201,7 @@ def _tuned_tile(a, b, row_scale, column_scale, bias, out, epilogue, residual, ta
     try:
         path = _cache_file(key)
         path.parent.mkdir(parents=True, exist_ok=True)
-        tmp = path.with_suffix(f".{os.getpid()}.tmp")
+        tmp = path.with_suffix(f".{os.getpid()}.{threading.get_ident()}.tmp")
         tmp.write_text(json.dumps(_encode(best)))
         tmp.replace(path)
     except OSError:
