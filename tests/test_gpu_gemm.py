@@ -295,14 +295,16 @@ def test_c4_shapes_beyond_2gib():
 
 
 @pytest.mark.parametrize("m,n,k", [(1024, 768, 1024), (16385, 5376, 7168), (20000, 2560, 384),
-                                   (8200, 2056, 256)])
+                                   (8200, 2056, 256), (8200, 2052, 384)])
 def test_int8_tma_entry_matches_int8_matmul(m, n, k):
     """model/int8_tma.py:33-41's entry point (the persistent GEMM): same output
     as int8_matmul, and the reference's tile tuples map onto HIP tiles. The
     long-M shapes (the reference's M >= 16384 regime) give each of the 256
     workgroups 3-6 tiles, with M and N tails; 8200 x 2056 x 256 gives some
     workgroups a second tile two k-steps long (the shortest streamed loop),
-    after a full tile or an edge tile, and checks the GELU epilogue too."""
+    after a full tile or an edge tile, and checks the GELU epilogue too;
+    N = 2052 (not a multiple of 8) runs the loop with the direct-store
+    epilogue over several tiles per workgroup."""
     from lynnreal_omni_amd import int8_tma
     g = gen(16 + m)
     a = torch.randint(-127, 128, (m, k), dtype=torch.int8, generator=g).cuda()
