@@ -1096,8 +1096,8 @@ __global__ __launch_bounds__(512) void gemm_stream(GemmArgs p) {
     };
     // The schedule of gemm_fast's ping-pong loop. A later tile's k-steps 0
     // and 1 were issued by the tile before it, whose last waits (A(KT) and
-    // W(KT)) covered k-step 0; the first waits in the loop (k-step 1 landed)
-    // skip the previous tile's output stores where their count is known.
+    // W(KT)) covered k-step 0; with the staged epilogue k-step 1 has landed
+    // too, and the loop skips its wait after k-step 0 (kWaitAll above).
     if (grp == 0) {
       if (first) {
         pdma_a(0);
