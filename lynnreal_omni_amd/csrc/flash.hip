@@ -99,16 +99,22 @@ __global__ __launch_bounds__(kThreads) void restore_rows_any(const uint16_t* __r
 }
 
 // ------------------------------------------------------ nearest anchor ----
-// For dropped row d (thread), over anchors a in increasing order: skip those
-// whose time pos[a, 0] differs from pos[d, 0]; keep the first a with the
-// smallest (h_d - h_a)^2 + (w_d - w_a)^2. Coordinates are fp32 (the
-// reference casts positions with .float()); the distance is formed in fp64,
-// whose rounding lies far below the fp32 spacing of the coordinates, and
-// exact ties (integer or dyadic grids) resolve to the first anchor, as
-// torch's argmin does. No anchor of the same time leaves a = 0, as argmin
-// over a row of +inf does. Then inverse[dropped[d]] = inverse[anchors[a]]. Row numbers
-// past `tokens` are clamped, like the gather's indices.
+// For dropped row d, over anchors a in increasing order: skip those whose
+// time pos[a, 0] differs from pos[d, 0]; keep the first a with the smallest
+// (h_d - h_a)^2 + (w_d - w_a)^2. Coordinates are fp32 (the reference casts
+// positions with .float()); the distance is formed in fp64, whose rounding
+// lies far below the fp32 spacing of the coordinates, and exact ties (integer
+// or dyadic grids) resolve to the first anchor, as torch's argmin does. No
+// anchor of the same time leaves a = 0, as argmin over a row of +inf does.
+// Then inverse[dropped[d]] = inverse[anchors[a]]. Row numbers past `tokens`
+// are clamped, like the gather's indices.
+//
+// One wave per dropped row: lane l scans anchors l, l + 64, ... of each tile
+// of anchor positions staged in LDS for the block's rows, keeping its first
+// nearest one, and a wave minimum over (distance, anchor index) then gives
+// the first nearest anchor of all.
 constexpr int kAnchorTile = 1024;
+constexpr int kAnchorRows = kThreads / 64;  // dropped rows per block
 
 __global__ __launch_bounds__(kThreads) void nearest_anchor(const float* __restrict__ pos,
                                                            const int64_t* __restrict__ dropped,
@@ -117,7 +123,8 @@ __global__ __launch_bounds__(kThreads) void nearest_anchor(const float* __restri
                                                            int64_t tokens, int64_t n_dropped,
                                                            int64_t n_anchors) {
   __shared__ float tt[kAnchorTile], th[kAnchorTile], tw[kAnchorTile];
-  const int64_t d = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int64_t d = (int64_t)blockIdx.x * kAnchorRows + wave;
   const bool live = d < n_dropped;
   const int64_t row = live ? clamp_index(dropped[d], tokens) : 0;
   const float t0 = live ? pos[3 * row] : 0.0f;
@@ -135,7 +142,7 @@ __global__ __launch_bounds__(kThreads) void nearest_anchor(const float* __restri
       tw[j] = pos[3 * a + 2];
     }
     __syncthreads();
-    for (int j = 0; j < n; ++j) {
+    for (int j = lane; j < n; j += 64) {
       if (tt[j] != t0) continue;
       const double dh = h0 - (double)th[j], dw = w0 - (double)tw[j];
       const double dist = dh * dh + dw * dw;
@@ -145,7 +152,18 @@ __global__ __launch_bounds__(kThreads) void nearest_anchor(const float* __restri
       }
     }
   }
-  if (live) inverse[row] = inverse[clamp_index(anchors[best_a], tokens)];
+  // The first anchor of the smallest distance over the wave; lanes that found
+  // none hold (+inf, 0), so a row with no anchor of its time keeps a = 0.
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    const double od = __shfl_xor(best, off);
+    const int64_t oa = __shfl_xor(best_a, off);
+    if (od < best || (od == best && oa < best_a)) {
+      best = od;
+      best_a = oa;
+    }
+  }
+  if (live && lane == 0) inverse[row] = inverse[clamp_index(anchors[best_a], tokens)];
 }
 
 }  // namespace
@@ -214,7 +232,7 @@ extern "C" int lr_flash_nearest_anchor(const float* positions, int64_t tokens,
   if (n_dropped == 0) return LR_OK;
   LR_REQUIRE(n_anchors > 0 && tokens > 0, "nearest_anchor: dropped rows but no anchors");
   LR_REQUIRE(positions && dropped && anchors && inverse, "nearest_anchor: null pointer");
-  const int64_t blocks = (n_dropped + kThreads - 1) / kThreads;
+  const int64_t blocks = (n_dropped + kAnchorRows - 1) / kAnchorRows;
   LR_REQUIRE(blocks <= 0x7fffffffLL, "nearest_anchor: too many rows");
   hipLaunchKernelGGL(nearest_anchor, dim3((unsigned)blocks), dim3(kThreads), 0, as_stream(stream),
                      positions, dropped, anchors, inverse, tokens, n_dropped, n_anchors);

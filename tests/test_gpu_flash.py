@@ -136,3 +136,46 @@ def test_hooks_reproduce_compress_and_restore():
     for b in blocks[6:]:
         h = b(h, temb, indices, rotary, mask)
     assert torch.equal(got, h)
+
+
+def _first_nearest(pos, dropped, anchors):
+    """Brute force over anchors in increasing order: the first anchor of the
+    row's time with the smallest squared (h, w) distance in fp64, else 0."""
+    out = []
+    for d in dropped:
+        best, best_a = np.inf, 0
+        for i, a in enumerate(anchors):
+            if pos[a, 0] != pos[d, 0]:
+                continue
+            dist = (float(pos[d, 1]) - float(pos[a, 1])) ** 2 + (float(pos[d, 2]) - float(pos[a, 2])) ** 2
+            if dist < best:
+                best, best_a = dist, i
+        out.append(best_a)
+    return np.array(out)
+
+
+def test_nearest_anchor_entry_point_ties_tiles_and_lonely_rows():
+    """lr_flash_nearest_anchor directly: 3000 anchors (three LDS tiles, the
+    nearest one in any lane's share), integer coordinates with many exact ties
+    (the first anchor wins), and dropped rows of a time with no anchor (they
+    take anchor 0)."""
+    from lynnreal_omni_amd import _lib
+    g = torch.Generator().manual_seed(21)
+    tokens = 4200
+    pos = torch.zeros(tokens, 3, dtype=torch.float32)
+    pos[:, 0] = torch.randint(0, 4, (tokens,), generator=g).float()
+    pos[:, 1:] = torch.randint(0, 40, (tokens, 2), generator=g).float()
+    order = torch.randperm(tokens, generator=g)
+    anchors = order[:3000].sort().values
+    dropped = order[3000:].sort().values
+    pos[dropped[:50], 0] = 9.0  # a time with no anchor
+    inverse = torch.arange(tokens, dtype=torch.int64) * 7 + 3
+    pos_d, anchors_d, dropped_d, inverse_d = pos.cuda(), anchors.cuda(), dropped.cuda(), inverse.cuda()
+    _lib.call("lr_flash_nearest_anchor", pos_d.data_ptr(), tokens, dropped_d.data_ptr(), dropped.numel(),
+              anchors_d.data_ptr(), anchors.numel(), inverse_d.data_ptr(), _lib.stream(pos_d))
+    torch.cuda.synchronize()
+    pick = _first_nearest(pos.numpy(), dropped.numpy(), anchors.numpy())
+    want = inverse.numpy().copy()
+    want[dropped.numpy()] = inverse.numpy()[anchors.numpy()[pick]]
+    assert (pick[:50] == 0).all()
+    assert np.array_equal(inverse_d.cpu().numpy(), want)
