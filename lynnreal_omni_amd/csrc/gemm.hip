@@ -1426,12 +1426,21 @@ int auto_tile(int64_t m, int64_t n, int64_t k) {
     if (tiles(LR_TILE_64x80) <= (m > 128 ? cus : cus / 2)) return LR_TILE_64x80;
     if (m > 128 && tiles(LR_TILE_128x160) <= cus) return LR_TILE_128x160;
   }
+  // Relative cost of a wave of tiles (one per CU; two per CU for 128x128).
+  // The 192-row and 192-column tiles hold the same outputs; 192x256 runs the
+  // 2x4 wave grid, whose W refill goes out a phase earlier than the 4x2 grid
+  // of 256x192, and is taken unless it needs more waves. Graph-replayed at
+  // K = 5120 on M = 512-6144, N = 5120-20480 and K = 20480 on N = 5120, these
+  // weights pick the fastest tile or one within 0.6% on all 24 shapes (M =
+  // 2048, N = 5120: 47.0 us against 48.0 for 256x192; M = 4096, N = 5120:
+  // 90.4 us against 97.4 for 128x128, whose wave is 0.74 of a 192-row one).
   auto waves = [&](int t, int64_t slots) { return (tiles(t) + slots - 1) / slots; };
+  const int64_t w192w = waves(LR_TILE_256x192, cus), w192t = waves(LR_TILE_192x256, cus);
   const int64_t c256 = waves(LR_TILE_256x256, cus) * 66;
-  const int64_t c192 = waves(LR_TILE_256x192, cus) * 60;
-  const int64_t c128 = waves(LR_TILE_128x128, 2 * cus) * 36;
-  const int64_t c64 = waves(LR_TILE_64x128, cus) * 18;
-  if (c192 < c256 && c192 < c128 && c192 < c64) return LR_TILE_256x192;
+  const int64_t c192 = (w192t <= w192w ? w192t : w192w) * 60;
+  const int64_t c128 = waves(LR_TILE_128x128, 2 * cus) * 44;
+  const int64_t c64 = waves(LR_TILE_64x128, cus) * 22;
+  if (c192 < c256 && c192 < c128 && c192 < c64) return w192t <= w192w ? LR_TILE_192x256 : LR_TILE_256x192;
   if (c256 <= c128 && c256 <= c64) {
     // 192x256 against 256x256 by per-tile time a + b*K (us, fitted at K = 5120
     // and 20480 on M = 12288, N = 5120): a longer K spreads 192x256's larger
