@@ -1406,14 +1406,13 @@ int tile_cols(int tile) {
   }
 }
 
-// Shape heuristic from measured sweeps on MI355X (256 CUs, K = 5120, M from
-// 64 to 12288, N from 5120 to 20480). A launch takes as many waves of tiles
-// as its tile count fills the resident blocks (one 256x256, 256x192 or 64x128
-// block per CU, two 128x128 blocks), and a wave of K = 5120 tiles took about
-// 66 us (256x256), 60 us (256x192), 36 us (128x128) and 18 us (64x128): the
-// shape with the fewest wave-microseconds wins, ties to the larger tile
-// (256x192 only when strictly better: M = 2048, N = 5120 runs 216 of its
-// tiles in one wave, 60 us against 67 us for 160 tiles of 256x256).
+// Shape heuristic from measured sweeps on MI355X (256 CUs, K = 5120 and
+// 20480, M from 64 to 12288, N from 5120 to 20480). A launch takes as many
+// waves of tiles as its tile count fills the resident blocks (one 256x256,
+// 192x256, 256x192 or 64x128 block per CU, two 128x128 blocks); each wave
+// costs a weight per tile (below), and the fewest weighted waves win, ties to
+// the larger tile. Past that, 256x256 and 192x256 are compared by a per-tile
+// time in K (long K favours 192x256 when it fills the waves better).
 int auto_tile(int64_t m, int64_t n, int64_t k) {
   const int64_t cus = 256;
   auto tiles = [&](int t) { return ((m + tile_rows(t) - 1) / tile_rows(t)) * ((n + tile_cols(t) - 1) / tile_cols(t)); };
