@@ -1418,11 +1418,17 @@ int auto_tile(int64_t m, int64_t n, int64_t k) {
   auto tiles = [&](int t) { return ((m + tile_rows(t) - 1) / tile_rows(t)) * ((n + tile_cols(t) - 1) / tile_cols(t)); };
   // A few hundred rows (graph-replay timings at K = 5120): 64x80 when its
   // tiles fit one wave (M = 256, N = 5120: 14.6 us against 16.2 us for
-  // 64x128; M = 64, N = 5120: 12.5 against 13.7), else 128x160 when its tiles
-  // fit one wave (M = 256, N = 20480: 29 us against 34 us for 256x80 and
-  // 38 us for 128x128). At M <= 128 with wide N the 64x128 tile stays ahead.
+  // 64x128; M = 128, N = 10240: 14.7 against 16.6; M = 96, N = 7168: 13.7
+  // against 14.9), except a nearly full wave at M <= 64, where 64x128 is 3%
+  // ahead (M = 64, N = 20480: 19.2 against 19.8 us). Where 64x80 tiles spill
+  // past one wave but 64x128 tiles fit it, 64x128 (M = 256, N = 5376: 168
+  // tiles, 19.5 us against 28.8 us for 128x160's 68 tiles at K = 7168, 35.3
+  // against 51.5 us at K = 14336). Else 128x160 when its tiles fit one wave
+  // (M = 256, N = 20480: 29 us against 34 us for 256x80 and 38 us for
+  // 128x128).
   if (m <= 256) {
-    if (tiles(LR_TILE_64x80) <= (m > 128 ? cus : cus / 2)) return LR_TILE_64x80;
+    if (tiles(LR_TILE_64x80) <= (m <= 64 ? cus * 3 / 4 : cus)) return LR_TILE_64x80;
+    if (tiles(LR_TILE_64x128) <= cus) return LR_TILE_64x128;
     if (m > 128 && tiles(LR_TILE_128x160) <= cus) return LR_TILE_128x160;
   }
   // Relative cost of a wave of tiles (one per CU; two per CU for 128x128).
