@@ -860,30 +860,54 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_fast(GemmArgs p) 
 // 16-byte chunks XOR-swizzled by row) instead of the whole tile at once.
 // K % 128 == 0 and K >= 256.
 
-// The pass-staged epilogue of one wave's 128x64 sub-tile (N % 8 == 0 and
-// 16-byte aligned outputs, as for store_tile_staged): pass p stages rows
-// 32p .. 32p + 31 (fragments 2p and 2p + 1) in the MFMA layout, then each lane
-// finishes and stores 4 whole 16-byte chunks of them.
+// The pass-staged epilogue of one wave's 128x64 sub-tile (N % 8 == 0,
+// N <= 2^21 and 16-byte aligned outputs): pass p stages rows 32p .. 32p + 31
+// (fragments 2p and 2p + 1) in the MFMA layout, then each lane finishes and
+// stores 4 whole 16-byte chunks of them.
+//
+// Scales, bias and outputs go through buffer ranges that start at the tile's
+// first row and column and end at M and N: loads past them return zero and
+// stores past them are dropped, so no load or store needs a per-row check or a
+// 64-bit address. A lane whose columns lie past N stores at byte offset 2^31
+// and up, beyond every range (a tile's output range is under 2^30 bytes).
 template <int EPI, bool BIAS>
 __device__ __forceinline__ void store_tile_passes(const GemmArgs& p, const v4i (&acc)[8][4], char* stage,
                                                   int64_t m0, int64_t n0, int wm, int wn, int lane) {
   constexpr int FM = 8, FN = 4, WM = 128, WN = 64;
   const int lr_ = lane & 15, lg = lane >> 4;
+  const int64_t tile_rows = min((int64_t)256, p.m - m0), tile_cols = min((int64_t)256, p.n - n0);
+  const __amdgpu_buffer_rsrc_t r_rs = row_rsrc(p.rs + m0, tile_rows * 4);
+  const __amdgpu_buffer_rsrc_t r_cs = row_rsrc(p.cs + n0, tile_cols * 4);
   float rsv[FM];
   float4 csv[FN];
   uint2 bv[FN];
+  const uint32_t rs_off = (uint32_t)(wm * WM + lr_) * 4;
 #pragma unroll
-  for (int i = 0; i < FM; ++i) {
-    const int64_t row = m0 + wm * WM + 16 * i + lr_;
-    rsv[i] = p.rs[row < p.m ? row : p.m - 1];
-  }
+  for (int i = 0; i < FM; ++i)
+    rsv[i] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r_rs, rs_off + 64 * i, 0, 0));
+  const uint32_t cs_off = (uint32_t)(wn * WN + 4 * lg) * 4;
 #pragma unroll
   for (int j = 0; j < FN; ++j) {
-    const int64_t col = n0 + wn * WN + 16 * j + 4 * lg;
-    const int64_t c = col < p.n ? col : p.n - 4;  // N % 8 == 0 on this path
-    csv[j] = *reinterpret_cast<const float4*>(p.cs + c);
-    if (BIAS) bv[j] = *reinterpret_cast<const uint2*>(p.bias + c);
+    const v4u c = __builtin_amdgcn_raw_buffer_load_b128(r_cs, cs_off + 64 * j, 0, 0);
+    csv[j] = make_float4(__uint_as_float(c.x), __uint_as_float(c.y), __uint_as_float(c.z),
+                         __uint_as_float(c.w));
   }
+  if (BIAS) {
+    const __amdgpu_buffer_rsrc_t r_b = row_rsrc(p.bias + n0, tile_cols * 2);
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+      const v2u b = __builtin_amdgcn_raw_buffer_load_b64(r_b, cs_off / 2 + 32 * j, 0, 0);
+      bv[j] = make_uint2(b.x, b.y);
+    }
+  }
+  // Output offsets (non-gated): lane l stores the 16-byte chunk l % 8 of row
+  // l / 8 of each group of 8 rows.
+  const __amdgpu_buffer_rsrc_t r_c =
+      row_rsrc(static_cast<const uint16_t*>(p.c) + m0 * p.n, tile_rows * p.n * 2);
+  const int64_t out_col = n0 + wn * WN + (lane & 7) * 8;
+  const uint32_t c_off = out_col < p.n ? (uint32_t)(((wm * WM + (lane >> 3)) * p.n + out_col) * 2)
+                                       : 0x80000000u;
+  const uint32_t rows8 = (uint32_t)(16 * p.n);  // bytes of 8 output rows
   // Everything issued before these loads, the next tile's first operand DMAs
   // among them, has landed once they have (gemm_stream's k-loop relies on it).
   __builtin_amdgcn_s_waitcnt(0x70 | 0xf00);  // vmcnt(0)
@@ -926,12 +950,12 @@ __device__ __forceinline__ void store_tile_passes(const GemmArgs& p, const v4i (
       for (int b = 0; b < BATCH; ++b) {
         const int q = (s0 + b) * 64 + lane;
         const int r = q >> 3, ch = q & 7;
-        const int64_t row = m0 + wm * WM + 32 * pass + r;
-        const int64_t col = n0 + wn * WN + ch * 8;
-        ok[b] = row < p.m && col < p.n;
-        o[b] = row * p.n + col;
         v[b] = *reinterpret_cast<const uint4*>(stage + r * 128 + ((ch ^ (r & 7)) << 4));
         if (EPI == EPI_GATED) {
+          const int64_t row = m0 + wm * WM + 32 * pass + r;
+          const int64_t col = n0 + wn * WN + ch * 8;
+          ok[b] = row < p.m && col < p.n;
+          o[b] = row * p.n + col;
           // Clamped (always valid) addresses, so that no load sits under a branch.
           const int64_t row_l = ok[b] ? row : m0, col_l = ok[b] ? col : n0;
           const int64_t tr = clamp_index(
@@ -955,7 +979,13 @@ __device__ __forceinline__ void store_tile_passes(const GemmArgs& p, const v4i (
           }
           if (w == 0) v[b].x = y; else if (w == 1) v[b].y = y; else if (w == 2) v[b].z = y; else v[b].w = y;
         }
-        if (ok[b]) store_c16(static_cast<uint16_t*>(p.c) + o[b], v[b]);
+        if (EPI == EPI_GATED) {
+          if (ok[b]) store_c16(static_cast<uint16_t*>(p.c) + o[b], v[b]);
+        } else {
+          const v4u w = {v[b].x, v[b].y, v[b].z, v[b].w};
+          __builtin_amdgcn_raw_buffer_store_b128(w, r_c, c_off + (uint32_t)(4 * pass + s0 + b) * rows8, 0,
+                                                 2 /* nt */);
+        }
       }
     }
     // This pass's chunks are in registers before the next pass overwrites them.
@@ -1291,7 +1321,7 @@ void launch_persistent(GemmArgs& p, hipStream_t st) {
   const int64_t cus = compute_units() >= 8 ? compute_units() / 8 * 8 : 8;
   const dim3 grid((unsigned)(tiles < cus ? tiles : cus));
   if constexpr (EPI != EPI_RAW) {
-    if (p.staged) {
+    if (p.staged && p.n <= (1 << 21)) {  // the pass-staged epilogue's byte offsets stay below 2^31
       hipLaunchKernelGGL((gemm_stream<EPI, BIAS, true>), grid, dim3(512), 0, st, p);
       return;
     }
@@ -1408,13 +1438,14 @@ int tile_cols(int tile) {
 
 // Shape heuristic from measured sweeps on MI355X (256 CUs, K = 5120 and
 // 20480, M from 64 to 12288, N from 5120 to 20480). A launch takes as many
-// waves of tiles as its tile count fills the resident blocks (one 256x256,
-// 192x256, 256x192 or 64x128 block per CU, two 128x128 blocks); each wave
+// waves of tiles as its tile count fills the resident blocks of the device's
+// CUs (one 256x256, 192x256, 256x192 or 64x128 block per CU, two 128x128
+// blocks; a partitioned GPU has fewer CUs per device); each wave
 // costs a weight per tile (below), and the fewest weighted waves win, ties to
 // the larger tile. Past that, 256x256 and 192x256 are compared by a per-tile
 // time in K (long K favours 192x256 when it fills the waves better).
 int auto_tile(int64_t m, int64_t n, int64_t k) {
-  const int64_t cus = 256;
+  const int64_t cus = compute_units();
   auto tiles = [&](int t) { return ((m + tile_rows(t) - 1) / tile_rows(t)) * ((n + tile_cols(t) - 1) / tile_cols(t)); };
   // A few hundred rows (graph-replay timings at K = 5120): 64x80 when its
   // tiles fit one wave (M = 256, N = 5120: 14.6 us against 16.2 us for
@@ -1458,7 +1489,8 @@ int auto_tile(int64_t m, int64_t n, int64_t k) {
 }
 
 // Split-K for a few hundred rows at long K, on 128x160 tiles: as many slices
-// as keep the workgroups within one wave of 256 CUs, at most 4 (1 = no split).
+// as keep the workgroups within one wave of the device's CUs, at most 4 (1 =
+// no split).
 // Graph-replayed at M = 256, N = 5120, K = 20480 (bf16 + bias): 35.6 us for
 // 128x160 in 4 slices against 41.8 us unsplit on the shape's own tile. At
 // K = 5120 every split measured slower than the unsplit small-M tiles (the
@@ -1467,7 +1499,7 @@ int auto_tile(int64_t m, int64_t n, int64_t k) {
 int auto_splits(int64_t m, int64_t n, int64_t k) {
   if (m > 256 || k < 16384 || k % 128 != 0 || n % 4 != 0) return 1;
   const int64_t tiles = ((m + 127) / 128) * ((n + 159) / 160);
-  int64_t s = 256 / tiles;
+  int64_t s = compute_units() / tiles;
   if (s > 4) s = 4;
   return s > 1 ? (int)s : 1;
 }
