@@ -61,10 +61,16 @@
 #define GEMM_SKINNY_NB 3
 #endif
 #ifndef GEMM_SKINNY64_NA
-#define GEMM_SKINNY64_NA 8
+#define GEMM_SKINNY64_NA 4
 #endif
 #ifndef GEMM_SKINNY64_NB
-#define GEMM_SKINNY64_NB 8
+#define GEMM_SKINNY64_NB 4
+#endif
+#ifndef GEMM_SKINNY128_NA
+#define GEMM_SKINNY128_NA 4
+#endif
+#ifndef GEMM_SKINNY128_NB
+#define GEMM_SKINNY128_NB 4
 #endif
 // Staging rows whose residual and gate chunks the gated epilogue loads
 // before using any of them, where it divides the wave's rows of chunks (else
@@ -1353,20 +1359,22 @@ void launch_fast(int tile, GemmArgs& p, hipStream_t st) {
     // tiles, not by LDS or MFMA.
     // Weight-streaming tiles for a few hundred rows: 4 waves of 64x80 (or
     // 16x80). 256x80 makes one wave of tiles from N = 20480 at M <= 256, 64x80
-    // one wave from N = 5120 at M <= 256. They are bound by the latency of the
-    // DMA stream: 4 + 3 slots (158 KB) for 256x80 (A re-read from L2 by every
-    // CU dominates), and 8 + 8 (144 KB) for 64x80, both rings 7 k-steps ahead
-    // (A is L2-resident, W comes from HBM). Graph-replayed at N = K = 5120:
-    // 14.5-14.9 us at M = 256 against 15.3-15.6 for 4 + 12, and 11.8-12.2
-    // against 12.6-12.7 at M = 64; splits such as 6 + 10, 9 + 7 and 10 + 6
-    // measured about 20% slower than either.
+    // one wave from N = 5120 at M <= 256. 256x80 takes 4 + 3 slots (158 KB; A
+    // re-read from L2 by every CU dominates). 64x80 takes 4 + 4 (72 KB, both
+    // rings 3 k-steps ahead). Graph-replayed at N = K = 5120, forced 64x80:
+    // 13.7-13.8 us at M = 256 against 14.3 for 8 + 8, 11.2-11.3 against 11.8
+    // at M = 64, 4-5% on every shape measured from M = 1 to 256. Where the
+    // tiles spill past one wave, two 72 KB blocks share a CU: M = 256,
+    // N = 5376, K = 7168 26.7 against 31.2 us. 2 + 2 runs 60% slower; 4 + 8,
+    // 8 + 4 and 8 + 8 land between; 6 + 6 and 7 + 7 are 12-20% slower than
+    // 8 + 8, and so were 6 + 10, 9 + 7 and 10 + 6 on an earlier build.
     case LR_TILE_256x80: launch_fast_cfg<256, 80, GEMM_SKINNY_WAVES, 1, EPI, BIAS, GEMM_SKINNY_NA, GEMM_SKINNY_NB>(p, st); break;
     case LR_TILE_64x80: launch_fast_cfg<64, 80, 4, 1, EPI, BIAS, GEMM_SKINNY64_NA, GEMM_SKINNY64_NB>(p, st); break;
     // 4 waves of 64x80 over 128 rows: one wave of tiles from N = 20480 at
     // M <= 256 that moves 36 KB per k-step against 44 KB for 256x80 (every CU
     // re-reads its A rows from L2): 29 against 34 us at M = 256. 4 + 4 slots
     // (144 KB).
-    case LR_TILE_128x160: launch_fast_cfg<128, 160, 2, 2, EPI, BIAS, 4, 4>(p, st); break;
+    case LR_TILE_128x160: launch_fast_cfg<128, 160, 2, 2, EPI, BIAS, GEMM_SKINNY128_NA, GEMM_SKINNY128_NB>(p, st); break;
     // 8 waves of 96x64 (the 2x4 grid, so the early W refill): where 256x256
     // tiles leave the last wave a quarter empty (M = 12288, N = 5120: 960
     // tiles = 3.75 waves) its 1280 tiles make 5 full waves. Each tile carries
