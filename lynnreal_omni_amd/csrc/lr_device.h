@@ -55,7 +55,10 @@ __device__ __forceinline__ uint4 buf_load16_reused(__amdgpu_buffer_rsrc_t r, uin
 // fused norm + quant from 42 to 38 us and the 5120-wide quantizer from 31 to
 // 29 us; 16-byte stores (bf16 rows) write through to system scope (sc0 sc1),
 // 4% faster for the bf16 norm, where nt made it 10% slower. Either way no
-// dirty output lines are left in L2 for the end-of-kernel write-back.
+// dirty output lines are left in L2 for the end-of-kernel write-back. Inside
+// the projection chain, write-back int8 stores ran both norms 3-5 us faster
+// but left the step time level (3.120-3.125 ms either way): the dirty lines'
+// write-back lands in the GEMM that follows.
 constexpr int kStore16Policy = 0x11;  // sc0 | sc1
 constexpr int kStore8Policy = 0x2;    // nt
 __device__ __forceinline__ void buf_store16(__amdgpu_buffer_rsrc_t r, uint32_t voff,
